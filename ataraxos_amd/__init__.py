@@ -1,0 +1,25 @@
+"""MI355X (gfx950) attention hot path of the ataraxos transformer networks.
+
+* :class:`MultiHeadAttention` — drop-in for ``stratego.networks.attention.MultiHeadAttention``;
+  its GPU path is one fused HIP kernel (``libataraxos_attn.so``).
+* :class:`KeyQueryPolicyHead` — drop-in for the Move network's policy head,
+  with the logits, legal-move mask and softmax fused on the GPU.
+* :class:`KVCache` / :func:`ops.attention_decode` — incremental causal decode.
+
+Importing the package does not load the library or touch the GPU.
+"""
+
+from . import ops
+from .attention import MultiHeadAttention, math_attention
+from .decode import KVCache
+from .policy import KeyQueryPolicyHead, masked_policy_logits, masked_policy_softmax
+
+__all__ = [
+    "ops",
+    "MultiHeadAttention",
+    "math_attention",
+    "KeyQueryPolicyHead",
+    "masked_policy_logits",
+    "masked_policy_softmax",
+    "KVCache",
+]

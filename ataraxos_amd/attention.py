@@ -1,0 +1,151 @@
+"""Drop-in ``MultiHeadAttention`` whose GPU path is the gfx950 fused kernel.
+
+Interface parity with ``stratego/networks/attention.py:64-204``:
+
+* constructor ``(embed_dim, num_heads, num_kv_heads=None, dropout=0.0,
+  causal=False, qkv_bias=False)`` with the same ``ValueError`` checks
+  (attention.py:97-103);
+* attributes ``embed_dim, num_heads, num_kv_heads, head_dim, dropout,
+  causal`` and submodules ``q_proj, k_proj, v_proj, out_proj`` created in that
+  order, so ``state_dict`` keys and the RNG draws of their initialisation are
+  the reference's (attention.py:105-116);
+* ``forward(x, key_value=None)``: projections, BSHD views, causal masking only
+  for self-attention, output projection (attention.py:152-204).
+
+Backends (``backend`` property, the slot of attention.py:122-146):
+
+* ``"hip"``  — tensors on a GPU: the fused HIP kernel (``ops.attention``).
+  Its range is head_dim a multiple of 16 up to 128 and at most 256 keys;
+  outside that the forward raises instead of switching to another path.
+* ``"math"`` — tensors on the CPU, or training with ``dropout > 0`` (the
+  kernel has no dropout, as the reference's FA3 backend has none:
+  attention.py:134-138).  It keeps the semantics of attention.py:281-316.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import cast
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F  # noqa: N812
+
+from . import ops
+
+__all__ = ["MultiHeadAttention", "math_attention"]
+
+
+def math_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    is_causal: bool,
+    dropout_p: float = 0.0,
+    scale: float | None = None,
+    key_padding_mask: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Unfused attention with the semantics of attention.py:281-316.
+
+    q ``[B, S_q, H, D]``, k/v ``[B, S_kv, H_kv, D]`` -> ``[B, S_q, H, D]``.
+    The scale multiplies the product after the matmul; the causal mask is
+    top-left aligned (``triu(ones(S_q, S_kv), 1)`` set to -inf); KV heads are
+    repeated per query group as ``repeat_interleave`` does.
+    """
+    n_heads, n_kv = q.shape[2], k.shape[2]
+    qh, kh, vh = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    if n_kv != n_heads:
+        kh = kh.repeat_interleave(n_heads // n_kv, dim=1)
+        vh = vh.repeat_interleave(n_heads // n_kv, dim=1)
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    scores = torch.matmul(qh, kh.transpose(-2, -1).contiguous()) * scale
+    if is_causal:
+        above = torch.ones(q.shape[1], k.shape[1], dtype=torch.bool, device=q.device).triu(1)
+        scores = scores.masked_fill(above, float("-inf"))
+    if key_padding_mask is not None:
+        scores = scores.masked_fill(key_padding_mask[:, None, None, :], float("-inf"))
+    probs = F.softmax(scores, dim=-1)
+    if dropout_p > 0.0:
+        probs = F.dropout(probs, p=dropout_p)
+    return torch.matmul(probs, vh).transpose(1, 2)
+
+
+class MultiHeadAttention(nn.Module):
+    """Multi-head / grouped-query attention; see the module docstring."""
+
+    def __init__(
+        self,
+        embed_dim: int,
+        num_heads: int,
+        num_kv_heads: int | None = None,
+        dropout: float = 0.0,
+        causal: bool = False,
+        qkv_bias: bool = False,
+    ) -> None:
+        super().__init__()
+        if embed_dim % num_heads != 0:
+            raise ValueError(f"embed_dim ({embed_dim}) must be divisible by num_heads ({num_heads})")
+        kv_heads = num_heads if num_kv_heads is None else num_kv_heads
+        if num_heads % kv_heads != 0:
+            raise ValueError(f"num_heads ({num_heads}) must be divisible by num_kv_heads ({kv_heads})")
+
+        self.embed_dim = embed_dim
+        self.num_heads = num_heads
+        self.num_kv_heads: int = kv_heads
+        self.head_dim: int = embed_dim // num_heads
+        self.dropout: float = dropout
+        self.causal: bool = causal
+
+        kv_dim = kv_heads * self.head_dim
+        self.q_proj = nn.Linear(embed_dim, num_heads * self.head_dim, bias=qkv_bias)
+        self.k_proj = nn.Linear(embed_dim, kv_dim, bias=qkv_bias)
+        self.v_proj = nn.Linear(embed_dim, kv_dim, bias=qkv_bias)
+        self.out_proj = nn.Linear(num_heads * self.head_dim, embed_dim, bias=qkv_bias)
+
+    @property
+    def backend(self) -> str:
+        """``"hip"`` on a GPU, ``"math"`` on the CPU or when dropout must run."""
+        device = next(self.parameters()).device
+        if device.type != "cuda":
+            return "math"
+        if self.training and self.dropout > 0.0:
+            return "math"
+        return "hip"
+
+    def forward(self, x: torch.Tensor, key_value: torch.Tensor | None = None) -> torch.Tensor:
+        """``x`` ``[B, S_q, E]``; ``key_value`` ``[B, S_kv, E]`` or None -> ``[B, S_q, E]``."""
+        batch, seq_q, _ = x.shape
+        src = x if key_value is None else key_value
+        q = self.q_proj(x).view(batch, seq_q, self.num_heads, self.head_dim)
+        k = self.k_proj(src)
+        seq_kv = k.shape[1]
+        k = k.view(batch, seq_kv, self.num_kv_heads, self.head_dim)
+        v = self.v_proj(src).view(batch, seq_kv, self.num_kv_heads, self.head_dim)
+        is_causal = self.causal and key_value is None
+
+        if self.backend == "hip":
+            attn = self._forward_hip(q, k, v, is_causal)
+        else:
+            attn = self._forward_math(q, k, v, is_causal)
+        return cast(torch.Tensor, self.out_proj(attn.reshape(batch, seq_q, self.embed_dim)))
+
+    def _expand_kv_heads(self, k: torch.Tensor, v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Repeat ``(B, H_kv, S, D)`` KV heads up to ``H`` (attention.py:210-220)."""
+        if self.num_kv_heads == self.num_heads:
+            return k, v
+        rep = self.num_heads // self.num_kv_heads
+        return k.repeat_interleave(rep, dim=1), v.repeat_interleave(rep, dim=1)
+
+    def _forward_hip(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, is_causal: bool) -> torch.Tensor:
+        """Fused gfx950 kernel on the BSHD views; GQA is indexed, not expanded."""
+        if not ops.attention_supported(self.head_dim, k.shape[1], q.dtype):
+            raise RuntimeError(
+                f"MultiHeadAttention: the HIP kernel does not cover head_dim={self.head_dim}, "
+                f"seq_kv={k.shape[1]}, dtype={q.dtype} (head_dim in {ops.HEAD_DIMS}, seq_kv <= {ops.MAX_SEQ_KV})"
+            )
+        return ops.attention(q, k, v, causal=is_causal)
+
+    def _forward_math(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, is_causal: bool) -> torch.Tensor:
+        p = self.dropout if (self.training and self.dropout > 0.0) else 0.0
+        return math_attention(q, k, v, is_causal, dropout_p=p)

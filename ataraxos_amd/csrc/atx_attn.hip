@@ -1,0 +1,619 @@
+// Fused attention forward for gfx950 (MI355X).
+//
+// Semantics follow the math fallback of the reference,
+// stratego/networks/attention.py:281-316: S = (Q K^T) * scale, top-left causal
+// mask (torch.triu(ones(S_q, S_kv), 1) -> -inf), softmax over keys, O = P V,
+// with GQA mapping query head h to KV head h / (H / H_kv) as the
+// repeat_interleave of attention.py:210-220 does.
+//
+// One workgroup (4 waves) owns one (batch, head) pair.  The whole key range
+// (<= 256 keys) is resident at once, so the softmax is computed in a single
+// pass from registers: no running-max rescaling.
+//
+// Work layout (16-bit types, MFMA v_mfma_f32_16x16x32_{bf16,f16}):
+//   * K rows are staged in LDS, row stride 2*D+16 bytes (an odd number of
+//     16-byte units, so the 16 rows an MFMA operand read touches fall in
+//     distinct bank groups).
+//   * V is staged TRANSPOSED in LDS (V^T[d][key]) because the PV product
+//     reduces over keys and the MFMA wants the reduction index contiguous per
+//     lane.  Keys are permuted inside each 32-key chunk so that the 8 keys one
+//     lane needs for one PV MFMA are one 16-byte block, and blocks are
+//     XOR-swizzled by the reading lane's row so the 16 lanes of a read hit 16
+//     distinct bank groups.
+//   * Each wave takes 16-query tiles.  Per tile it computes S^T = K Q^T
+//     (keys on MFMA rows, queries on columns): lane (m = l%16, g = l/16) then
+//     holds query m against keys 16*kt + 4*g + i, i.e. one query per lane, so
+//     the row softmax needs only in-lane work plus two cross-lane steps.
+//   * P (bf16/fp16) feeds O^T = V^T P^T as the B operand straight from
+//     registers.  MFMA row r of output tile dt stands for head-dim index
+//     (r/4)*(D/4) + 4*dt + r%4, which leaves every lane with D/4 contiguous
+//     outputs of one query, stored with wide writes.
+#include "atx_common.hpp"
+
+namespace atx {
+
+struct AttnArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    int64_t qsb, qss, qsh;
+    int64_t ksb, kss, ksh;
+    int64_t vsb, vss, vsh;
+    int64_t osb, oss, osh;
+    const uint8_t* kpad;
+    int64_t kpsb;
+    int H, group, Sq, Skv, nkt;
+    float c2;  // scale * log2(e)
+    int causal;
+};
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+
+// Per-lane bitmask of usable keys (bit 4*kt + i <-> key 16*kt + 4*g + i):
+// inside the key range and not padded out.
+__device__ inline uint64_t key_valid_bits(const AttnArgs& a, int b, int g, int nkt) {
+    uint64_t bits = 0;
+    const uint8_t* row = a.kpad ? a.kpad + (int64_t)b * a.kpsb : nullptr;
+    for (int kt = 0; kt < nkt; ++kt) {
+        for (int i = 0; i < 4; ++i) {
+            int key = kt * 16 + 4 * g + i;
+            bool ok = key < a.Skv;
+            if (ok && row) ok = row[key] == 0;
+            if (ok) bits |= (uint64_t)1 << (4 * kt + i);
+        }
+    }
+    return bits;
+}
+
+// Waves per SIMD that the register allocator is asked to fit, per head_dim
+// (rows: 16, 32, 48, 64, 80, 96, 112, 128) and 32-key chunk count (columns:
+// NKC = 1..8).  Each entry is the highest target for which hipcc (ROCm 7.2,
+// gfx950) produced the kernel without register spills; the AMDGPU scheduler
+// is not monotonic in this target (a looser budget can make it hoist loads
+// far enough to spill), so the values were found by compiling every
+// instantiation at every target, not by a formula.
+constexpr int kOcc16[8][8] = {
+    {8, 7, 8, 7, 5, 5, 4, 4}, {8, 7, 8, 7, 5, 5, 4, 4}, {8, 6, 8, 6, 5, 4, 4, 4}, {8, 7, 8, 6, 5, 4, 4, 4},
+    {8, 6, 7, 5, 5, 4, 4, 4}, {8, 6, 3, 5, 5, 4, 3, 3}, {7, 6, 3, 5, 4, 3, 3, 2}, {6, 5, 3, 3, 4, 3, 3, 2},
+};
+constexpr int kOcc32[8][8] = {
+    {8, 8, 7, 5, 4, 4, 3, 3}, {8, 8, 6, 5, 4, 4, 3, 3}, {8, 7, 5, 4, 4, 3, 3, 3}, {8, 7, 5, 4, 4, 3, 3, 2},
+    {8, 7, 5, 4, 4, 3, 3, 2}, {8, 6, 5, 4, 4, 3, 3, 2}, {8, 6, 4, 4, 3, 3, 3, 2}, {7, 5, 4, 4, 3, 3, 3, 2},
+};
+template <int D, int NKC>
+constexpr int occ_16bit() {
+    return kOcc16[D / 16 - 1][NKC - 1];
+}
+template <int D, int NKC>
+constexpr int occ_fp32() {
+    return kOcc32[D / 16 - 1][NKC - 1];
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit inputs (bf16 / fp16): NKC = number of 32-key chunks (S_kv <= 32*NKC).
+// ---------------------------------------------------------------------------
+template <typename T, int D, int NKC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(occ_16bit<D, NKC>(), 8)))
+void attn_fwd_16bit(AttnArgs a) {
+    using M = Mfma16<T>;
+    constexpr int CH = D / 8;          // 16-byte chunks per row
+    constexpr int NI = (D + 31) / 32;  // QK^T MFMAs per 16x16 tile
+    constexpr int NDT = D / 16;        // PV output tiles
+    constexpr int QD = D / 4;          // contiguous outputs per lane
+    constexpr int RS = D * 2 + 16;     // K row stride in LDS (bytes)
+    constexpr int NB = (4 * NKC <= 16) ? 16 : 32;  // 16-byte blocks per V^T row
+    constexpr int RSV = NB * 16;
+    constexpr int NKT = 2 * NKC;
+
+    const int nkt = a.nkt;  // 2*NKC or 2*NKC - 1
+    lds_t* const sk = lds_base();
+    lds_t* const svt = sk + nkt * 16 * RS;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int m = lane & 15, g = lane >> 4;
+    const int bh = blockIdx.x;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int hk = h / a.group;
+
+    const T* kb = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
+    const T* vb = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
+    const T* qb = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
+    T* ob = static_cast<T*>(a.o) + b * a.osb + h * a.osh;
+
+    const int nqt = (a.Sq + 15) >> 4;
+
+    // Q operand of this wave's first tile, issued before the staging loads.
+    auto load_q = [&](int qt, u32x4 (&qop)[NI]) {
+        const int qrow = qt * 16 + m;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int c = 4 * i + g;
+            qop[i] = (qrow < a.Sq && c < CH) ? ld16(qb + qrow * a.qss + c * 8) : u32x4{0, 0, 0, 0};
+        }
+    };
+    u32x4 qop[NI];
+    if (wave < nqt) load_q(wave, qop);
+
+    // ---- stage K (row-major, padded rows) --------------------------------
+    constexpr int KIT = (NKT * 16 * CH + kThreads - 1) / kThreads;
+    u32x4 kreg[KIT];
+    const int kchunks = a.Skv * CH;
+#pragma unroll
+    for (int it = 0; it < KIT; ++it) {
+        const int idx = tid + it * kThreads;
+        if (idx < kchunks) {
+            const int r = idx / CH, c = idx - (idx / CH) * CH;
+            kreg[it] = ld16(kb + r * a.kss + c * 8);
+        }
+    }
+    // ---- stage V^T: task = (4-key quad, 8-wide d chunk) ------------------
+    constexpr int VT = 8 * NKC * CH;
+    constexpr int VIT = (VT + kThreads - 1) / kThreads;
+    u32x4 vreg[VIT][4];
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+        const int t = tid + it * kThreads;
+        const int dc = t % CH, kq = t / CH;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int key = 4 * kq + j;
+            vreg[it][j] = (t < VT && key < a.Skv) ? ld16(vb + key * a.vss + dc * 8) : u32x4{0, 0, 0, 0};
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < KIT; ++it) {
+        const int idx = tid + it * kThreads;
+        if (idx < kchunks) {
+            const int r = idx / CH, c = idx - (idx / CH) * CH;
+            lds_st16(sk + r * RS + c * 16, kreg[it]);
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+        const int t = tid + it * kThreads;
+        if (t < VT) {
+            const int dc = t % CH, kq = t / CH;
+            const int key0 = 4 * kq;
+            const int w = key0 & 31;
+            const int lb = 4 * (key0 >> 5) + ((w & 15) >> 2);  // logical block
+            const int boff = (w >> 4) * 8;                      // byte offset in block
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t x0 = vreg[it][0][e], x1 = vreg[it][1][e];
+                const uint32_t x2 = vreg[it][2][e], x3 = vreg[it][3][e];
+                const u32x2 even = {(x0 & 0xffffu) | (x1 << 16), (x2 & 0xffffu) | (x3 << 16)};
+                const u32x2 odd = {(x0 >> 16) | (x1 & 0xffff0000u), (x2 >> 16) | (x3 & 0xffff0000u)};
+                const int d0 = dc * 8 + 2 * e, d1 = d0 + 1;
+                const int h0 = ((d0 / QD) << 2) | (d0 & 3), h1 = ((d1 / QD) << 2) | (d1 & 3);
+                lds_st8(svt + d0 * RSV + ((lb ^ h0) << 4) + boff, even);
+                lds_st8(svt + d1 * RSV + ((lb ^ h1) << 4) + boff, odd);
+            }
+        }
+    }
+
+    const bool masked_path = a.causal || a.kpad != nullptr;
+    uint64_t kbits = 0;
+    if (masked_path) kbits = key_valid_bits(a, b, g, nkt);
+    const bool last_full = (nkt == NKT);
+    __syncthreads();
+
+    const float c2 = a.c2;
+    const float kNegInf = -__builtin_inff();
+
+    for (int qt = wave; qt < nqt; qt += kWaves) {
+        const int qrow = qt * 16 + m;
+        lds_t* const skq = lds_opaque(sk);
+        lds_t* const svq = lds_opaque(svt);
+
+        // ---- S^T = K Q^T over the key tiles -----------------------------
+        f32x4 s[NKT];
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+            s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (kt < NKT - 1 || last_full) {
+                const lds_t* krow = skq + (kt * 16 + m) * RS;
+#pragma unroll
+                for (int i = 0; i < NI; ++i) {
+                    const int c = 4 * i + g;
+                    u32x4 kop = lds_ld16(krow + c * 16);
+                    if (CH % 4 != 0 && c >= CH) kop = u32x4{0, 0, 0, 0};
+                    s[kt] = M::mma(kop, qop[i], s[kt]);
+                }
+            }
+        }
+        // Prefetch the next tile's Q operand while the softmax runs.
+        if (qt + kWaves < nqt) load_q(qt + kWaves, qop);
+        // Phase fences: keep the scheduler from hoisting the PV operand reads
+        // above the softmax, which would hold both phases' registers at once.
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- mask ---------------------------------------------------------
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+            const bool partial = (kt * 16 + 16 > a.Skv);
+            if (masked_path) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = kt * 16 + 4 * g + i;
+                    bool ok = (kbits >> (4 * kt + i)) & 1;
+                    if (a.causal) ok = ok && key <= qrow;
+                    s[kt][i] = ok ? s[kt][i] : kNegInf;
+                }
+            } else if (partial) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = kt * 16 + 4 * g + i;
+                    s[kt][i] = key < a.Skv ? s[kt][i] : kNegInf;
+                }
+            }
+        }
+
+        // ---- single-pass softmax over the whole key row -------------------
+        float mx = kNegInf;
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][i]);
+        mx = colgroup_max(mx);
+        // A fully masked row has mx = -inf; -mb = +inf then makes every
+        // exponent NaN, which is what softmax over an all -inf row returns.
+        const float mb = mx * c2;
+
+        float lsum = 0.f;
+        u32x4 pk[NKC];
+#pragma unroll
+        for (int c = 0; c < NKC; ++c) {
+            float p[8];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int kt = 2 * c + hh;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float e = fast_exp2(__builtin_fmaf(s[kt][i], c2, -mb));
+                    if (kt == NKT - 1 && !last_full) e = 0.f;
+                    p[4 * hh + i] = e;
+                    lsum += e;
+                }
+            }
+            pk[c] = u32x4{M::pack2(p[0], p[1]), M::pack2(p[2], p[3]), M::pack2(p[4], p[5]),
+                          M::pack2(p[6], p[7])};
+        }
+        lsum = colgroup_sum(lsum);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- O^T = V^T P^T -----------------------------------------------
+        f32x4 oacc[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int d = (m >> 2) * QD + dt * 4 + (m & 3);
+            const lds_t* vrow = svq + d * RSV;
+#pragma unroll
+            for (int c = 0; c < NKC; ++c) {
+                const u32x4 vop = lds_ld16(vrow + (((4 * c + g) ^ m) << 4));
+                oacc[dt] = M::mma(vop, pk[c], oacc[dt]);
+            }
+        }
+
+        // ---- normalise and store D/4 contiguous outputs per lane ----------
+        if (qrow < a.Sq) {
+            const float inv = fast_rcp(lsum);
+            T* orow = ob + qrow * a.oss + g * QD;
+            if constexpr (QD % 8 == 0) {
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt += 2) {
+                    const u32x4 w = {M::pack2(oacc[dt][0] * inv, oacc[dt][1] * inv),
+                                     M::pack2(oacc[dt][2] * inv, oacc[dt][3] * inv),
+                                     M::pack2(oacc[dt + 1][0] * inv, oacc[dt + 1][1] * inv),
+                                     M::pack2(oacc[dt + 1][2] * inv, oacc[dt + 1][3] * inv)};
+                    st16(orow + dt * 4, w);
+                }
+            } else {
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    const u32x2 w = {M::pack2(oacc[dt][0] * inv, oacc[dt][1] * inv),
+                                     M::pack2(oacc[dt][2] * inv, oacc[dt][3] * inv)};
+                    st8(orow + dt * 4, w);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 inputs: v_mfma_f32_16x16x4_f32 keeps full fp32 products.  K operands
+// come straight from global memory (L1/L2); only V^T is staged in LDS.
+// ---------------------------------------------------------------------------
+template <int D, int NKC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(occ_fp32<D, NKC>(), 8)))
+void attn_fwd_fp32(AttnArgs a) {
+    constexpr int CH = D / 4;    // 16-byte chunks (4 floats) per row
+    constexpr int NI = D / 16;   // chunk groups per 16x16 tile
+    constexpr int NDT = D / 16;
+    constexpr int QD = D / 4;
+    constexpr int NKT = 2 * NKC;
+    constexpr int NB = (8 * NKC <= 16) ? 16 : (8 * NKC <= 32 ? 32 : 64);  // 4-key blocks per V^T row
+    constexpr int RSV = NB * 16;
+
+    lds_t* const svt = lds_base();
+
+    const int nkt = a.nkt;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int m = lane & 15, g = lane >> 4;
+    const int bh = blockIdx.x;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int hk = h / a.group;
+
+    const float* kb = static_cast<const float*>(a.k) + b * a.ksb + hk * a.ksh;
+    const float* vb = static_cast<const float*>(a.v) + b * a.vsb + hk * a.vsh;
+    const float* qb = static_cast<const float*>(a.q) + b * a.qsb + h * a.qsh;
+    float* ob = static_cast<float*>(a.o) + b * a.osb + h * a.osh;
+
+    // ---- stage V^T: task = (4-key quad, 4-wide d chunk) ------------------
+    constexpr int VT = 8 * NKC * CH;
+    const int nkq = 4 * nkt;  // quads that the PV loop reads
+    for (int t = tid; t < VT; t += kThreads) {
+        const int dc = t % CH, kq = t / CH;
+        if (kq >= nkq) continue;
+        u32x4 x[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int key = 4 * kq + j;
+            x[j] = key < a.Skv ? ld16(vb + key * a.vss + dc * 4) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int d = dc * 4 + e;
+            const int hd = ((d / QD) << 2) | (d & 3);
+            const u32x4 col = {x[0][e], x[1][e], x[2][e], x[3][e]};
+            lds_st16(svt + d * RSV + ((kq ^ hd) << 4), col);
+        }
+    }
+    const bool masked_path = a.causal || a.kpad != nullptr;
+    uint64_t kbits = 0;
+    if (masked_path) kbits = key_valid_bits(a, b, g, nkt);
+    __syncthreads();
+
+    const float c2 = a.c2;
+    const float kNegInf = -__builtin_inff();
+    const int nqt = (a.Sq + 15) >> 4;
+
+    for (int qt = wave; qt < nqt; qt += kWaves) {
+        const int qrow = qt * 16 + m;
+        lds_t* const svq = lds_opaque(svt);
+        u32x4 qop[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            qop[i] = qrow < a.Sq ? ld16(qb + qrow * a.qss + (4 * i + g) * 4) : u32x4{0, 0, 0, 0};
+
+        f32x4 s[NKT];
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+            s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (kt < nkt) {
+                int krow = kt * 16 + m;
+                krow = krow < a.Skv ? krow : a.Skv - 1;  // rows past the end are masked below
+#pragma unroll
+                for (int i = 0; i < NI; ++i) {
+                    const f32x4 kop = as_f32x4(ld16(kb + krow * a.kss + (4 * i + g) * 4));
+                    const f32x4 qv = as_f32x4(qop[i]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) s[kt] = mma_f32(kop[j], qv[j], s[kt]);
+                }
+            }
+        }
+
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = kt * 16 + 4 * g + i;
+                bool ok = key < a.Skv;
+                if (masked_path) {
+                    ok = (kbits >> (4 * kt + i)) & 1;
+                    if (a.causal) ok = ok && key <= qrow;
+                }
+                s[kt][i] = ok ? s[kt][i] : kNegInf;
+            }
+        }
+
+        float mx = kNegInf;
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][i]);
+        mx = colgroup_max(mx);
+        const float mb = mx * c2;
+        float lsum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float e = fast_exp2(__builtin_fmaf(s[kt][i], c2, -mb));
+                if (kt >= nkt) e = 0.f;
+                s[kt][i] = e;
+                lsum += e;
+            }
+        lsum = colgroup_sum(lsum);
+        __builtin_amdgcn_sched_barrier(0);
+
+        f32x4 oacc[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int d = (m >> 2) * QD + dt * 4 + (m & 3);
+            const lds_t* vrow = svq + d * RSV;
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt) {
+                if (kt < nkt) {
+                    const f32x4 vop = as_f32x4(lds_ld16(vrow + (((4 * kt + g) ^ m) << 4)));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) oacc[dt] = mma_f32(vop[i], s[kt][i], oacc[dt]);
+                }
+            }
+        }
+
+        if (qrow < a.Sq) {
+            // Exact division keeps the fp32 path within a few ulp of the
+            // reference's softmax normalisation.
+            float* orow = ob + qrow * a.oss + g * QD;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const f32x4 r = {oacc[dt][0] / lsum, oacc[dt][1] / lsum, oacc[dt][2] / lsum, oacc[dt][3] / lsum};
+                st16(orow + dt * 4, __builtin_bit_cast(u32x4, r));
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch
+// ---------------------------------------------------------------------------
+namespace {
+
+template <typename Kernel>
+int launch(Kernel kernel, int grid, size_t lds, hipStream_t stream, const AttnArgs& args) {
+    if (lds > 64 * 1024) {
+        // Above the 64 KiB default the dynamic LDS size must be raised per kernel.
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) ATX_FAIL(ATX_ERR_LAUNCH, "hipFuncSetAttribute(%zu bytes LDS): %s", lds, hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), lds, stream, args);
+    ATX_CHECK_LAUNCH("atx_attn_fwd launch");
+    return ATX_OK;
+}
+
+template <typename T, int D>
+int dispatch_16bit(int nkc, int grid, hipStream_t st, const AttnArgs& a) {
+    const size_t k_lds = (size_t)a.nkt * 16 * (D * 2 + 16);
+    const size_t vt_lds = (size_t)D * ((4 * nkc <= 16) ? 16 : 32) * 16;
+    const size_t lds = k_lds + vt_lds;
+    switch (nkc) {
+        case 1: return launch(attn_fwd_16bit<T, D, 1>, grid, lds, st, a);
+        case 2: return launch(attn_fwd_16bit<T, D, 2>, grid, lds, st, a);
+        case 3: return launch(attn_fwd_16bit<T, D, 3>, grid, lds, st, a);
+        case 4: return launch(attn_fwd_16bit<T, D, 4>, grid, lds, st, a);
+        case 5: return launch(attn_fwd_16bit<T, D, 5>, grid, lds, st, a);
+        case 6: return launch(attn_fwd_16bit<T, D, 6>, grid, lds, st, a);
+        case 7: return launch(attn_fwd_16bit<T, D, 7>, grid, lds, st, a);
+        case 8: return launch(attn_fwd_16bit<T, D, 8>, grid, lds, st, a);
+    }
+    ATX_FAIL(ATX_ERR_UNSUPPORTED, "seq_kv chunk count %d", nkc);
+}
+
+template <int D>
+int dispatch_fp32(int nkc, int grid, hipStream_t st, const AttnArgs& a) {
+    const int nb = (8 * nkc <= 16) ? 16 : (8 * nkc <= 32 ? 32 : 64);
+    const size_t lds = (size_t)D * nb * 16;
+    switch (nkc) {
+        case 1: return launch(attn_fwd_fp32<D, 1>, grid, lds, st, a);
+        case 2: return launch(attn_fwd_fp32<D, 2>, grid, lds, st, a);
+        case 3: return launch(attn_fwd_fp32<D, 3>, grid, lds, st, a);
+        case 4: return launch(attn_fwd_fp32<D, 4>, grid, lds, st, a);
+        case 5: return launch(attn_fwd_fp32<D, 5>, grid, lds, st, a);
+        case 6: return launch(attn_fwd_fp32<D, 6>, grid, lds, st, a);
+        case 7: return launch(attn_fwd_fp32<D, 7>, grid, lds, st, a);
+        case 8: return launch(attn_fwd_fp32<D, 8>, grid, lds, st, a);
+    }
+    ATX_FAIL(ATX_ERR_UNSUPPORTED, "seq_kv chunk count %d", nkc);
+}
+
+template <typename T>
+int dispatch_dim(int D, int nkc, int grid, hipStream_t st, const AttnArgs& a) {
+    switch (D) {
+        case 16: return dispatch_16bit<T, 16>(nkc, grid, st, a);
+        case 32: return dispatch_16bit<T, 32>(nkc, grid, st, a);
+        case 48: return dispatch_16bit<T, 48>(nkc, grid, st, a);
+        case 64: return dispatch_16bit<T, 64>(nkc, grid, st, a);
+        case 80: return dispatch_16bit<T, 80>(nkc, grid, st, a);
+        case 96: return dispatch_16bit<T, 96>(nkc, grid, st, a);
+        case 112: return dispatch_16bit<T, 112>(nkc, grid, st, a);
+        case 128: return dispatch_16bit<T, 128>(nkc, grid, st, a);
+    }
+    ATX_FAIL(ATX_ERR_UNSUPPORTED, "head_dim %d", D);
+}
+
+int dispatch_dim_fp32(int D, int nkc, int grid, hipStream_t st, const AttnArgs& a) {
+    switch (D) {
+        case 16: return dispatch_fp32<16>(nkc, grid, st, a);
+        case 32: return dispatch_fp32<32>(nkc, grid, st, a);
+        case 48: return dispatch_fp32<48>(nkc, grid, st, a);
+        case 64: return dispatch_fp32<64>(nkc, grid, st, a);
+        case 80: return dispatch_fp32<80>(nkc, grid, st, a);
+        case 96: return dispatch_fp32<96>(nkc, grid, st, a);
+        case 112: return dispatch_fp32<112>(nkc, grid, st, a);
+        case 128: return dispatch_fp32<128>(nkc, grid, st, a);
+    }
+    ATX_FAIL(ATX_ERR_UNSUPPORTED, "head_dim %d", D);
+}
+
+// Every row of a [B, S, H, D] view starts on a 16-byte boundary.
+bool rows_aligned(const void* base, int64_t sb, int64_t ss, int64_t sh, int esize) {
+    return aligned16(base) && ((sb * esize) & 15) == 0 && ((ss * esize) & 15) == 0 && ((sh * esize) & 15) == 0;
+}
+
+}  // namespace
+}  // namespace atx
+
+extern "C" int atx_attn_fwd(const AtxAttnParams* p, void* stream) {
+    using namespace atx;
+    clear_error();
+    if (!p) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_fwd: params is NULL");
+    if (p->abi_version != ATX_ABI_VERSION)
+        ATX_FAIL(ATX_ERR_ABI, "atx_attn_fwd: abi_version %d, library is %d", p->abi_version, ATX_ABI_VERSION);
+    if (p->dtype != ATX_DTYPE_BF16 && p->dtype != ATX_DTYPE_FP16 && p->dtype != ATX_DTYPE_FP32)
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_fwd: unknown dtype %d", p->dtype);
+    if (p->batch < 1 || p->seq_q < 1 || p->seq_kv < 1 || p->num_heads < 1 || p->num_kv_heads < 1 || p->head_dim < 1)
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT,
+                 "atx_attn_fwd: sizes must be >= 1 (batch %d, seq_q %d, seq_kv %d, heads %d, kv_heads %d, head_dim %d)",
+                 p->batch, p->seq_q, p->seq_kv, p->num_heads, p->num_kv_heads, p->head_dim);
+    if (p->num_heads % p->num_kv_heads != 0)
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_fwd: num_heads %d not divisible by num_kv_heads %d",
+                 p->num_heads, p->num_kv_heads);
+    if (!p->q || !p->k || !p->v || !p->o) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_fwd: null tensor pointer");
+    if (!(p->scale > 0.f) || p->scale == __builtin_inff())
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_fwd: scale must be finite and > 0 (got %g)", (double)p->scale);
+    if (p->head_dim % 16 != 0 || p->head_dim > 128)
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_fwd: head_dim %d not supported (multiple of 16, <= 128)", p->head_dim);
+    if (p->seq_kv > 256)
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_fwd: seq_kv %d not supported (<= 256)", p->seq_kv);
+    const int64_t grid = (int64_t)p->batch * p->num_heads;
+    if (grid > 0x7fffffff) ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_fwd: batch*heads %lld too large", (long long)grid);
+    const int es = p->dtype == ATX_DTYPE_FP32 ? 4 : 2;
+    if (!rows_aligned(p->q, p->q_stride_b, p->q_stride_s, p->q_stride_h, es) ||
+        !rows_aligned(p->k, p->k_stride_b, p->k_stride_s, p->k_stride_h, es) ||
+        !rows_aligned(p->v, p->v_stride_b, p->v_stride_s, p->v_stride_h, es) ||
+        !rows_aligned(p->o, p->o_stride_b, p->o_stride_s, p->o_stride_h, es))
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_fwd: every Q/K/V/O row must start on a 16-byte boundary");
+
+    AttnArgs a;
+    a.q = p->q;
+    a.k = p->k;
+    a.v = p->v;
+    a.o = p->o;
+    a.qsb = p->q_stride_b; a.qss = p->q_stride_s; a.qsh = p->q_stride_h;
+    a.ksb = p->k_stride_b; a.kss = p->k_stride_s; a.ksh = p->k_stride_h;
+    a.vsb = p->v_stride_b; a.vss = p->v_stride_s; a.vsh = p->v_stride_h;
+    a.osb = p->o_stride_b; a.oss = p->o_stride_s; a.osh = p->o_stride_h;
+    a.kpad = p->key_pad;
+    a.kpsb = p->key_pad_stride_b;
+    a.H = p->num_heads;
+    a.group = p->num_heads / p->num_kv_heads;
+    a.Sq = p->seq_q;
+    a.Skv = p->seq_kv;
+    a.nkt = (p->seq_kv + 15) / 16;
+    a.c2 = p->scale * kLog2e;
+    a.causal = p->causal != 0;
+    const int nkc = (p->seq_kv + 31) / 32;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    switch (p->dtype) {
+        case ATX_DTYPE_BF16: return dispatch_dim<__bf16>(p->head_dim, nkc, (int)grid, st, a);
+        case ATX_DTYPE_FP16: return dispatch_dim<_Float16>(p->head_dim, nkc, (int)grid, st, a);
+        default: return dispatch_dim_fp32(p->head_dim, nkc, (int)grid, st, a);
+    }
+}

@@ -1,0 +1,146 @@
+// Shared helpers of the gfx950 attention library: error reporting on the
+// host, vector types and MFMA wrappers on the device.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ataraxos_attn.h"
+
+namespace atx {
+
+// ---------------------------------------------------------------------------
+// Host: thread-local error text behind atx_last_error().
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+// Records `code` with a formatted message and returns it.
+#define ATX_FAIL(code, ...)            \
+    do {                               \
+        ::atx::set_error(__VA_ARGS__); \
+        return (code);                 \
+    } while (0)
+
+// Launch check: converts a HIP error after a launch into ATX_ERR_LAUNCH.
+#define ATX_CHECK_LAUNCH(what)                                                \
+    do {                                                                      \
+        hipError_t e_ = hipGetLastError();                                    \
+        if (e_ != hipSuccess)                                                 \
+            ATX_FAIL(ATX_ERR_LAUNCH, "%s: %s", (what), hipGetErrorString(e_)); \
+    } while (0)
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------------------
+// Device: vector types.
+// ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// 16-bit element types that run on the 16x16x32 MFMA.
+template <typename T>
+struct Mfma16;
+
+template <>
+struct Mfma16<__bf16> {
+    static constexpr int kDtype = ATX_DTYPE_BF16;
+    __device__ static inline f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                      __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+    // Two floats -> packed pair, round to nearest even (v_cvt_pk_bf16_f32).
+    __device__ static inline uint32_t pack2(float lo, float hi) {
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        bf16x2 r;
+        r[0] = static_cast<__bf16>(lo);
+        r[1] = static_cast<__bf16>(hi);
+        return __builtin_bit_cast(uint32_t, r);
+    }
+    __device__ static inline float to_float(uint16_t bits) {
+        return __builtin_bit_cast(float, static_cast<uint32_t>(bits) << 16);
+    }
+};
+
+template <>
+struct Mfma16<_Float16> {
+    static constexpr int kDtype = ATX_DTYPE_FP16;
+    __device__ static inline f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                     __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+    __device__ static inline uint32_t pack2(float lo, float hi) {
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        f16x2 r;
+        r[0] = static_cast<_Float16>(lo);
+        r[1] = static_cast<_Float16>(hi);
+        return __builtin_bit_cast(uint32_t, r);
+    }
+    __device__ static inline float to_float(uint16_t bits) {
+        return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+    }
+};
+
+// Reinterpret a 16-byte chunk as four floats.  The whole vector is cast and
+// then indexed: hipcc's __builtin_bit_cast applied to one element of an
+// ext_vector_type (bit_cast<float>(v[i])) yields element 0 for every i.
+__device__ inline f32x4 as_f32x4(u32x4 v) { return __builtin_bit_cast(f32x4, v); }
+
+__device__ inline f32x4 mma_f32(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Lane-level helpers (wave64).
+__device__ inline int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+__device__ inline float shfl_xor(float v, int mask) {
+    int l = lane_id();
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((l ^ mask) << 2, __builtin_bit_cast(int, v)));
+}
+
+// Max / sum over the four lanes {l, l^16, l^32, l^48} that share an MFMA
+// output column.
+__device__ inline float colgroup_max(float v) {
+    v = fmaxf(v, shfl_xor(v, 16));
+    return fmaxf(v, shfl_xor(v, 32));
+}
+__device__ inline float colgroup_sum(float v) {
+    v += shfl_xor(v, 16);
+    return v + shfl_xor(v, 32);
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ inline float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// LDS byte pointer.  Kernels address their shared memory through this type so
+// that every access stays a ds_* instruction.
+typedef __attribute__((address_space(3))) char lds_t;
+
+__device__ inline lds_t* lds_base() {
+    extern __shared__ __attribute__((aligned(16))) char smem_dyn[];
+    return (lds_t*)smem_dyn;  // generic -> LDS address-space cast
+}
+
+// Returns `p` through an empty asm so the compiler cannot treat LDS reads that
+// use it as loop-invariant: without this, a loop over query tiles gets every
+// K and V^T operand read hoisted out of it and the kernel runs out of VGPRs.
+__device__ inline lds_t* lds_opaque(lds_t* p) {
+    asm volatile("" : "+v"(p));
+    return p;
+}
+
+__device__ inline u32x4 lds_ld16(const lds_t* p) { return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(p); }
+__device__ inline void lds_st16(lds_t* p, u32x4 v) { *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(p) = v; }
+__device__ inline void lds_st8(lds_t* p, u32x2 v) { *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(p) = v; }
+
+// 16-byte global load / store through the vector memory path.
+__device__ inline u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ inline void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ inline void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+}  // namespace atx

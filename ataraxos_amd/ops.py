@@ -1,0 +1,297 @@
+"""Torch-facing entry points of the gfx950 kernels.
+
+Every function here takes device tensors, checks them, and launches a kernel
+from ``libataraxos_attn.so`` on the current HIP stream.  There is no CPU or
+PyTorch substitute behind them: a CPU tensor, a missing library or a shape
+outside the kernels' range raises.
+
+* :func:`attention` — fused ``softmax(Q K^T * scale + mask) V`` on BSHD views
+  (the seam ``_forward_<backend>(q, k, v, is_causal)`` of
+  ``stratego/networks/attention.py:222-316``), differentiable.
+* :func:`kq_policy` — the key-query policy head's logits, legal-move mask and
+  softmax (``stratego/networks/move_net.py:92-95`` plus the callers' softmax,
+  ``stratego/training/selfplay.py:284``).
+* :func:`attention_decode` — one query per (batch, head) against a KV cache.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+_DTYPES = {
+    torch.float32: _lib.DTYPE_FP32,
+    torch.bfloat16: _lib.DTYPE_BF16,
+    torch.float16: _lib.DTYPE_FP16,
+}
+
+MAX_SEQ_KV = 256
+HEAD_DIMS = (16, 32, 48, 64, 80, 96, 112, 128)
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require_device(name: str, *tensors: torch.Tensor) -> None:
+    dev = tensors[0].device
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise RuntimeError(f"{name}: expected GPU tensors, got a tensor on {t.device}")
+        if t.device != dev:
+            raise RuntimeError(f"{name}: tensors on different devices ({dev} vs {t.device})")
+
+
+def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
+    """Return ``t`` (or a contiguous copy) so that every row of its last dim
+    is contiguous and starts on a 16-byte boundary, as the kernels require."""
+    es = t.element_size()
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+    ok = ok and all((s * es) % 16 == 0 for s in t.stride()[:-1])
+    return t if ok else t.contiguous()
+
+
+def attention_supported(head_dim: int, seq_kv: int, dtype: torch.dtype) -> bool:
+    """True when :func:`attention` covers this shape and dtype."""
+    return dtype in _DTYPES and head_dim in HEAD_DIMS and 1 <= seq_kv <= MAX_SEQ_KV
+
+
+def attention_forward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    causal: bool = False,
+    scale: float | None = None,
+    key_padding_mask: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Forward only (no autograd).  q ``[B, S_q, H, D]``, k/v ``[B, S_kv, H_kv, D]``.
+
+    ``key_padding_mask`` is ``[B, S_kv]`` bool, True = ignore the key (the
+    ``key_padding_mask`` convention of ``torch.nn.MultiheadAttention``).
+    Returns ``[B, S_q, H, D]`` contiguous in q's dtype.
+    """
+    _require_device("attention", q, k, v)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("attention: q, k, v must be [batch, seq, heads, head_dim]")
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _DTYPES:
+        raise ValueError(f"attention: q/k/v dtypes {q.dtype}/{k.dtype}/{v.dtype} unsupported or mixed")
+    b, sq, h, d = q.shape
+    bk, skv, hkv, dk = k.shape
+    if bk != b or dk != d or tuple(v.shape) != (b, skv, hkv, d):
+        raise ValueError(f"attention: shape mismatch q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
+    if h % hkv != 0:
+        raise ValueError(f"attention: {h} query heads not divisible by {hkv} kv heads")
+    q, k, v = _aligned_rows(q), _aligned_rows(k), _aligned_rows(v)
+    if out is None:
+        out = torch.empty((b, sq, h, d), dtype=q.dtype, device=q.device)
+    elif tuple(out.shape) != (b, sq, h, d) or out.dtype != q.dtype or out.device != q.device:
+        raise ValueError("attention: out has the wrong shape, dtype or device")
+    pad = None
+    if key_padding_mask is not None:
+        if tuple(key_padding_mask.shape) != (b, skv):
+            raise ValueError(f"attention: key_padding_mask must be [{b}, {skv}]")
+        _require_device("attention", q, key_padding_mask)
+        pad = key_padding_mask.to(torch.uint8).contiguous()
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+
+    p = _lib.AttnParams()
+    p.abi_version = _lib.ABI_VERSION
+    p.dtype = _DTYPES[q.dtype]
+    p.batch, p.seq_q, p.seq_kv, p.num_heads, p.num_kv_heads, p.head_dim = b, sq, skv, h, hkv, d
+    p.q, (p.q_stride_b, p.q_stride_s, p.q_stride_h) = q.data_ptr(), q.stride()[:3]
+    p.k, (p.k_stride_b, p.k_stride_s, p.k_stride_h) = k.data_ptr(), k.stride()[:3]
+    p.v, (p.v_stride_b, p.v_stride_s, p.v_stride_h) = v.data_ptr(), v.stride()[:3]
+    p.o, (p.o_stride_b, p.o_stride_s, p.o_stride_h) = out.data_ptr(), out.stride()[:3]
+    p.scale = float(scale)
+    p.causal = 1 if causal else 0
+    p.key_pad = pad.data_ptr() if pad is not None else None
+    p.key_pad_stride_b = pad.stride(0) if pad is not None else 0
+    _lib.check(_lib.call("atx_attn_fwd", p, _stream(q)), "atx_attn_fwd")
+    return out
+
+
+def _attention_reference_fp32(q, k, v, causal, scale, key_padding_mask):
+    """Differentiable fp32 restatement used only to form gradients."""
+    b, sq, h, d = q.shape
+    skv, hkv = k.shape[1], k.shape[2]
+    qh = q.float().transpose(1, 2)
+    kh = k.float().transpose(1, 2)
+    vh = v.float().transpose(1, 2)
+    if hkv != h:
+        kh = kh.repeat_interleave(h // hkv, dim=1)
+        vh = vh.repeat_interleave(h // hkv, dim=1)
+    s = torch.matmul(qh, kh.transpose(-2, -1).contiguous()) * scale
+    if causal:
+        s = s.masked_fill(torch.ones(sq, skv, dtype=torch.bool, device=q.device).triu(1), float("-inf"))
+    if key_padding_mask is not None:
+        s = s.masked_fill(key_padding_mask[:, None, None, :], float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), vh).transpose(1, 2)
+
+
+class _HipAttention(torch.autograd.Function):
+    """HIP forward; the backward recomputes the attention in fp32 with torch
+    ops on the same device and differentiates that."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, causal, scale, key_padding_mask):  # type: ignore[override]
+        out = attention_forward(q, k, v, causal=causal, scale=scale, key_padding_mask=key_padding_mask)
+        ctx.save_for_backward(q, k, v)
+        ctx.causal, ctx.scale, ctx.kpm = causal, scale, key_padding_mask
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):  # type: ignore[override]
+        q, k, v = ctx.saved_tensors
+        with torch.enable_grad():
+            qf = q.detach().float().requires_grad_(True)
+            kf = k.detach().float().requires_grad_(True)
+            vf = v.detach().float().requires_grad_(True)
+            o = _attention_reference_fp32(qf, kf, vf, ctx.causal, ctx.scale, ctx.kpm)
+            gq, gk, gv = torch.autograd.grad(o, (qf, kf, vf), grad_out.float())
+        return gq.to(q.dtype), gk.to(k.dtype), gv.to(v.dtype), None, None, None
+
+
+def attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    causal: bool = False,
+    scale: float | None = None,
+    key_padding_mask: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Fused attention on BSHD tensors, with autograd (see :func:`attention_forward`)."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        return _HipAttention.apply(q, k, v, causal, scale, key_padding_mask)
+    return attention_forward(q, k, v, causal=causal, scale=scale, key_padding_mask=key_padding_mask)
+
+
+def kq_policy(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    legal_move_mask: torch.Tensor | None = None,
+    scale: float | None = None,
+    output: str = "probs",
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Policy over from x to squares for every sample.
+
+    q, k: ``[B, S, d]`` (from-queries, to-keys).  ``legal_move_mask``: bool
+    ``[B, S, S]``, True = legal.  ``scale`` defaults to ``1/sqrt(d)`` (the
+    reference divides by ``policy_d_model ** 0.5``).  ``output="probs"``
+    returns the softmax over all ``S*S`` entries with illegal entries exactly
+    0; ``output="logits"`` returns the scaled logits with illegal entries
+    -1e10.  Both are fp32 ``[B, S*S]`` in from-major order.
+    """
+    _require_device("kq_policy", q, k)
+    if q.dim() != 3 or q.shape != k.shape:
+        raise ValueError(f"kq_policy: q{tuple(q.shape)} and k{tuple(k.shape)} must both be [B, S, d]")
+    if q.dtype != k.dtype or q.dtype not in _DTYPES:
+        raise ValueError(f"kq_policy: unsupported or mixed dtypes {q.dtype}/{k.dtype}")
+    if output not in ("probs", "logits"):
+        raise ValueError(f"kq_policy: output must be 'probs' or 'logits', got {output!r}")
+    b, s, d = q.shape
+    q, k = _aligned_rows(q), _aligned_rows(k)
+    if out is None:
+        out = torch.empty((b, s * s), dtype=torch.float32, device=q.device)
+    elif tuple(out.shape) != (b, s * s) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("kq_policy: out must be a contiguous fp32 [B, S*S] tensor")
+    mask = None
+    if legal_move_mask is not None:
+        if tuple(legal_move_mask.shape) != (b, s, s):
+            raise ValueError(f"kq_policy: legal_move_mask must be [{b}, {s}, {s}]")
+        _require_device("kq_policy", q, legal_move_mask)
+        mask = legal_move_mask if legal_move_mask.dtype == torch.bool else legal_move_mask != 0
+        mask = mask.contiguous()
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+
+    p = _lib.KqParams()
+    p.abi_version = _lib.ABI_VERSION
+    p.dtype = _DTYPES[q.dtype]
+    p.batch, p.seq, p.dim = b, s, d
+    p.out_mode = _lib.KQ_OUT_PROBS if output == "probs" else _lib.KQ_OUT_LOGITS
+    p.q, p.q_stride_b, p.q_stride_s = q.data_ptr(), q.stride(0), q.stride(1)
+    p.k, p.k_stride_b, p.k_stride_s = k.data_ptr(), k.stride(0), k.stride(1)
+    p.mask = mask.data_ptr() if mask is not None else None
+    p.mask_stride_b = mask.stride(0) if mask is not None else 0
+    p.mask_stride_s = mask.stride(1) if mask is not None else 0
+    p.out, p.out_stride_b = out.data_ptr(), out.stride(0)
+    p.scale = float(scale)
+    _lib.check(_lib.call("atx_kq_masked_softmax_fwd", p, _stream(q)), "atx_kq_masked_softmax_fwd")
+    return out
+
+
+def attention_decode(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    kv_len: int | torch.Tensor,
+    k_new: torch.Tensor | None = None,
+    v_new: torch.Tensor | None = None,
+    scale: float | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """One decode step: q ``[B, H, D]`` against caches ``[B, H_kv, T, D]``.
+
+    ``kv_len`` is the number of valid cache rows after this step (an int, or a
+    device int32 tensor ``[B]`` of per-sample lengths).  With ``k_new`` /
+    ``v_new`` (``[B, H_kv, D]``) the row ``kv_len - 1`` is taken from them and
+    written into the caches in the same launch.  Returns ``[B, H, D]``.
+    """
+    tensors = [q, k_cache, v_cache] + [t for t in (k_new, v_new) if t is not None]
+    _require_device("attention_decode", *tensors)
+    if q.dim() != 3 or k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
+        raise ValueError("attention_decode: q must be [B, H, D] and caches [B, H_kv, T, D]")
+    b, h, d = q.shape
+    bc, hkv, cap, dc = k_cache.shape
+    if bc != b or dc != d or h % hkv != 0:
+        raise ValueError(f"attention_decode: q{tuple(q.shape)} does not match cache{tuple(k_cache.shape)}")
+    if any(t.dtype != q.dtype for t in tensors) or q.dtype not in _DTYPES:
+        raise ValueError("attention_decode: all tensors must share one supported dtype")
+    if (k_new is None) != (v_new is None):
+        raise ValueError("attention_decode: give k_new and v_new together")
+    for t in (k_cache, v_cache):
+        es = t.element_size()
+        if t.stride(-1) != 1 or t.data_ptr() % 16 or any((s * es) % 16 for s in t.stride()[:-1]):
+            raise ValueError("attention_decode: cache rows must be contiguous and 16-byte aligned")
+    q = _aligned_rows(q)
+    if k_new is not None:
+        if tuple(k_new.shape) != (b, hkv, d) or tuple(v_new.shape) != (b, hkv, d):
+            raise ValueError(f"attention_decode: k_new/v_new must be [{b}, {hkv}, {d}]")
+        k_new, v_new = _aligned_rows(k_new), _aligned_rows(v_new)
+    if out is None:
+        out = torch.empty((b, h, d), dtype=q.dtype, device=q.device)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+
+    p = _lib.DecodeParams()
+    p.abi_version = _lib.ABI_VERSION
+    p.dtype = _DTYPES[q.dtype]
+    p.batch, p.num_heads, p.num_kv_heads, p.head_dim = b, h, hkv, d
+    p.kv_capacity = cap
+    lens = None
+    if isinstance(kv_len, torch.Tensor):
+        _require_device("attention_decode", q, kv_len)
+        lens = kv_len.to(torch.int32).contiguous()
+        if tuple(lens.shape) != (b,):
+            raise ValueError(f"attention_decode: kv_len tensor must be [{b}]")
+        p.kv_len, p.kv_lens = 0, lens.data_ptr()
+    else:
+        p.kv_len, p.kv_lens = int(kv_len), None
+    p.q, p.q_stride_b, p.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    p.k_cache, (p.k_stride_b, p.k_stride_h, p.k_stride_s) = k_cache.data_ptr(), k_cache.stride()[:3]
+    p.v_cache, (p.v_stride_b, p.v_stride_h, p.v_stride_s) = v_cache.data_ptr(), v_cache.stride()[:3]
+    if k_new is not None:
+        p.k_new, p.k_new_stride_b, p.k_new_stride_h = k_new.data_ptr(), k_new.stride(0), k_new.stride(1)
+        p.v_new, p.v_new_stride_b, p.v_new_stride_h = v_new.data_ptr(), v_new.stride(0), v_new.stride(1)
+    p.o, p.o_stride_b, p.o_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    p.scale = float(scale)
+    _lib.check(_lib.call("atx_attn_decode_fwd", p, _stream(q)), "atx_attn_decode_fwd")
+    return out

@@ -1,0 +1,216 @@
+/*
+ * ataraxos_attn.h — C ABI of the MI355X (gfx950) attention library
+ * `libataraxos_attn.so`.
+ *
+ * The library holds the GPU side of the attention hot path of the ataraxos
+ * transformer networks (Move, Setup and Belief networks).  It has no libtorch
+ * dependency: every tensor crosses this boundary as a raw device pointer plus
+ * element strides, and every call is an asynchronous launch on the caller's
+ * HIP stream.
+ *
+ * Conventions shared by every entry point
+ *   - Return value: ATX_OK (0) on success, a negative ATX_ERR_* code on
+ *     failure.  No C++ exception crosses the boundary.  The text of the most
+ *     recent failure on the calling thread is available from atx_last_error().
+ *   - Memory: the caller allocates every buffer (inputs and outputs).  The
+ *     library allocates no device memory and keeps no mutable global state,
+ *     so calls are re-entrant and may run concurrently on different streams.
+ *   - Strides are in ELEMENTS, not bytes.  The innermost (head_dim / feature)
+ *     dimension must be contiguous (stride 1) and every row must start on a
+ *     16-byte boundary.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the legacy default
+ *     stream).  Nothing synchronises with the host.
+ *   - Argument validation happens on the host before any HIP call, so invalid
+ *     arguments are reported without touching a GPU.
+ */
+#ifndef ATARAXOS_ATTN_H
+#define ATARAXOS_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ATX_ABI_VERSION 1
+
+/* Return codes. */
+#define ATX_OK 0
+#define ATX_ERR_INVALID_ARGUMENT (-1) /* null pointer, bad size or stride */
+#define ATX_ERR_UNSUPPORTED (-2)      /* valid, but outside the kernels' range */
+#define ATX_ERR_LAUNCH (-3)           /* the HIP runtime rejected the launch */
+#define ATX_ERR_ABI (-4)              /* params struct from another ABI version */
+
+/* Element types. */
+#define ATX_DTYPE_FP32 0
+#define ATX_DTYPE_BF16 1
+#define ATX_DTYPE_FP16 2
+
+/* ------------------------------------------------------------------------ */
+/* Fused attention forward                                                  */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * O[b, s, h, :] = softmax_j( scale * Q[b, s, h, :] . K[b, j, h / G, :]
+ *                            + mask[b, s, j] ) . V[b, j, h / G, :]
+ * with G = num_heads / num_kv_heads (grouped-query attention) and mask = -inf
+ * where the key is padded out (key_pad[b, j] != 0) or, if `causal`, where
+ * j > s (top-left alignment, as torch.triu(ones(S_q, S_kv), 1)).
+ * A query row whose keys are all masked produces NaN, as a softmax over an
+ * all -inf row does.
+ *
+ * Q, K, V and O are BSHD tensors ([batch, seq, heads, head_dim], head_dim
+ * contiguous) given by base pointer and element strides; the Q/K/V views the
+ * reference takes of its [B, S, E] projection outputs are accepted as they
+ * are.  O is written in the same dtype as the inputs.
+ */
+typedef struct AtxAttnParams {
+    int32_t abi_version; /* must equal ATX_ABI_VERSION */
+    int32_t dtype;       /* ATX_DTYPE_*: Q, K, V and O all have this type */
+    int32_t batch;
+    int32_t seq_q;
+    int32_t seq_kv;
+    int32_t num_heads;    /* query heads H */
+    int32_t num_kv_heads; /* H_kv, divides H */
+    int32_t head_dim;     /* D */
+    const void* q;
+    int64_t q_stride_b, q_stride_s, q_stride_h;
+    const void* k;
+    int64_t k_stride_b, k_stride_s, k_stride_h;
+    const void* v;
+    int64_t v_stride_b, v_stride_s, v_stride_h;
+    void* o;
+    int64_t o_stride_b, o_stride_s, o_stride_h;
+    float scale;             /* > 0; the reference uses 1/sqrt(D) */
+    int32_t causal;          /* nonzero: mask j > s */
+    const uint8_t* key_pad;  /* optional [batch, seq_kv]; nonzero = ignore key */
+    int64_t key_pad_stride_b;
+} AtxAttnParams;
+
+/*
+ * Replaces the backend dispatch of MultiHeadAttention.forward and the four
+ * backend bodies it selects between:
+ *   stratego/networks/attention.py:192-200  (dispatch)
+ *   stratego/networks/attention.py:222-234  (_forward_fa3)
+ *   stratego/networks/attention.py:236-253  (_forward_fa2, dropout_p = 0)
+ *   stratego/networks/attention.py:255-279  (_forward_sdpa)
+ *   stratego/networks/attention.py:281-316  (_forward_math, the semantics)
+ * and the GQA expansion of stratego/networks/attention.py:210-220.
+ * The key-padding mask serves the Belief decoder's cross-attention
+ * (memory_key_padding_mask = ~hidden_mask, stratego/networks/belief_net.py:159).
+ *
+ * Supported range: dtype BF16, FP16 or FP32; head_dim a multiple of 16 up to
+ * 128; 1 <= seq_kv <= 256; any seq_q >= 1 and batch >= 1.
+ */
+int atx_attn_fwd(const AtxAttnParams* params, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Key-query policy head: logits + legal-move mask (+ softmax)              */
+/* ------------------------------------------------------------------------ */
+
+#define ATX_KQ_OUT_PROBS 0  /* softmax over all S*S entries, illegal = 0.0 */
+#define ATX_KQ_OUT_LOGITS 1 /* scaled logits, illegal = -1e10 */
+
+/*
+ * For every sample b, L[i, j] = scale * q[b, i, :] . k[b, j, :] over
+ * i, j < seq ("from" square i, "to" square j).  Entries whose mask byte is
+ * zero are illegal.  The output is fp32 [batch, seq * seq] in from-major
+ * order (index i * seq + j):
+ *   ATX_KQ_OUT_LOGITS: L, with illegal entries set to -1e10;
+ *   ATX_KQ_OUT_PROBS:  softmax of that over all seq*seq entries; illegal
+ *                      entries are exactly 0.0.  A sample with no legal
+ *                      entry gets the uniform 1/(seq*seq), which is what the
+ *                      softmax of an all -1e10 row gives.
+ * `mask` may be NULL (every entry legal).
+ */
+typedef struct AtxKqParams {
+    int32_t abi_version;
+    int32_t dtype; /* of q and k: ATX_DTYPE_BF16, FP16 or FP32 */
+    int32_t batch;
+    int32_t seq;   /* squares per sample, 1..128 */
+    int32_t dim;   /* policy_d_model, a multiple of 8 */
+    int32_t out_mode; /* ATX_KQ_OUT_* */
+    const void* q;
+    int64_t q_stride_b, q_stride_s;
+    const void* k;
+    int64_t k_stride_b, k_stride_s;
+    const uint8_t* mask; /* optional [batch, seq, seq]; nonzero = legal */
+    int64_t mask_stride_b, mask_stride_s;
+    float* out; /* [batch, seq * seq], contiguous per sample */
+    int64_t out_stride_b;
+    float scale; /* > 0; the reference divides by sqrt(policy_d_model) */
+} AtxKqParams;
+
+/*
+ * Replaces KeyQueryPolicyHead's logit product and mask,
+ *   stratego/networks/move_net.py:92-95,
+ * and (ATX_KQ_OUT_PROBS) the softmax its callers apply to the result:
+ *   stratego/training/selfplay.py:284, stratego/training/move_trainer.py:118,
+ *   stratego/search/rollouts.py:82, stratego/search/mirror_descent.py:126.
+ */
+int atx_kq_masked_softmax_fwd(const AtxKqParams* params, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Single-query attention over a KV cache (incremental decode)              */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * o[b, h, :] = softmax_{j < n_b}(scale * q[b, h, :] . K[b, h / G, j, :])
+ *              . V[b, h / G, j, :]
+ * with n_b = kv_lens[b] when kv_lens is given, else kv_len.  The cache rows
+ * are K[b, g, j, :] = k_cache + b*k_stride_b + g*k_stride_h + j*k_stride_s.
+ * When k_new / v_new are given ([batch, num_kv_heads, head_dim]), row n_b - 1
+ * is taken from them AND written into the cache, so one call appends the
+ * newest token and attends over it.  The result equals the last row of a full
+ * causal recompute over n_b tokens.
+ */
+typedef struct AtxDecodeParams {
+    int32_t abi_version;
+    int32_t dtype; /* ATX_DTYPE_BF16, FP16 or FP32, for every tensor */
+    int32_t batch;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim; /* a multiple of 8, up to 256 */
+    int32_t kv_capacity; /* rows allocated per cache head; lengths are clamped to it */
+    int32_t kv_len;   /* used when kv_lens is NULL; 1 <= kv_len <= kv_capacity */
+    const int32_t* kv_lens; /* optional device array [batch]; a length < 1 yields NaN */
+    const void* q;
+    int64_t q_stride_b, q_stride_h;
+    void* k_cache;
+    int64_t k_stride_b, k_stride_h, k_stride_s;
+    void* v_cache;
+    int64_t v_stride_b, v_stride_h, v_stride_s;
+    const void* k_new; /* optional, with v_new */
+    int64_t k_new_stride_b, k_new_stride_h;
+    const void* v_new;
+    int64_t v_new_stride_b, v_new_stride_h;
+    void* o;
+    int64_t o_stride_b, o_stride_h;
+    float scale;
+} AtxDecodeParams;
+
+/*
+ * No one-call counterpart in the reference: SetupNetwork re-runs its causal
+ * MultiHeadAttention over the whole prefix for every placed piece
+ * (stratego/training/selfplay.py:139-146,181 -> stratego/networks/
+ * setup_net.py:117 -> stratego/networks/attention.py:281-316 with
+ * is_causal = True).  This entry point returns the last row of that
+ * recompute from a KV cache.
+ */
+int atx_attn_decode_fwd(const AtxDecodeParams* params, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Library information                                                      */
+/* ------------------------------------------------------------------------ */
+
+/* Text of the last failure on the calling thread ("" if none). */
+const char* atx_last_error(void);
+
+/* ATX_ABI_VERSION of the built library. */
+int atx_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATARAXOS_ATTN_H */

@@ -1,0 +1,103 @@
+"""float64 numpy restatement of the reference attention math path (oracle).
+
+Test infrastructure only (see ``oracle/__init__.py``).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+NEG_INF = -np.inf
+
+
+def expand_kv_heads(x: np.ndarray, num_heads: int) -> np.ndarray:
+    """``[B, H_kv, S, D] -> [B, H, S, D]``: each KV head repeated ``H/H_kv``
+    times consecutively, so query head ``h`` reads KV head ``h // (H/H_kv)``.
+
+    Restates ``MultiHeadAttention._expand_kv_heads``
+    (stratego/networks/attention.py:210-220, ``repeat_interleave`` on dim 1).
+    """
+    group = num_heads // x.shape[1]
+    return x if group == 1 else np.repeat(x, group, axis=1)
+
+
+def softmax_lastdim(s: np.ndarray) -> np.ndarray:
+    """Max-shifted softmax over the last axis; an all ``-inf`` row gives NaN,
+    as ``torch.softmax`` does."""
+    m = s.max(axis=-1, keepdims=True)
+    with np.errstate(invalid="ignore"):
+        e = np.exp(s - m)
+        return e / e.sum(axis=-1, keepdims=True)
+
+
+def attention(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    causal: bool = False,
+    scale: float | None = None,
+    key_pad: np.ndarray | None = None,
+) -> np.ndarray:
+    """BSHD attention in float64.
+
+    q ``[B, S_q, H, D]``, k/v ``[B, S_kv, H_kv, D]`` -> ``[B, S_q, H, D]``.
+
+    Restates ``_forward_math`` (stratego/networks/attention.py:281-316):
+    transpose to BHSD (:293-296), expand KV heads (:299), scores
+    ``(Q K^T) * (1/sqrt(D))`` with the scale applied after the product
+    (:300-301), top-left causal mask ``triu(ones(S_q, S_kv), 1) -> -inf``
+    (:303-308), softmax over keys (:310), ``P V`` and back to BSHD (:315-316).
+    Dropout (:312-313) is inference-off and not restated.  ``key_pad``
+    (``[B, S_kv]``, True = ignore) adds the key-padding mask the Belief
+    decoder passes as ``memory_key_padding_mask`` (belief_net.py:159,172-177).
+    """
+    q64 = np.asarray(q, dtype=np.float64).transpose(0, 2, 1, 3)
+    k64 = np.asarray(k, dtype=np.float64).transpose(0, 2, 1, 3)
+    v64 = np.asarray(v, dtype=np.float64).transpose(0, 2, 1, 3)
+    num_heads, seq_q, head_dim = q64.shape[1], q64.shape[2], q64.shape[3]
+    seq_kv = k64.shape[2]
+    k64 = expand_kv_heads(k64, num_heads)
+    v64 = expand_kv_heads(v64, num_heads)
+    if scale is None:
+        scale = 1.0 / np.sqrt(head_dim)
+    scores = np.matmul(q64, k64.swapaxes(-1, -2)) * scale
+    if causal:
+        above = np.triu(np.ones((seq_q, seq_kv), dtype=bool), 1)
+        scores = np.where(above, NEG_INF, scores)
+    if key_pad is not None:
+        scores = np.where(np.asarray(key_pad, dtype=bool)[:, None, None, :], NEG_INF, scores)
+    return np.matmul(softmax_lastdim(scores), v64).transpose(0, 2, 1, 3)
+
+
+def linear(x: np.ndarray, weight: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+    """``x W^T + b`` as ``torch.nn.Linear`` (weight ``[out, in]``)."""
+    y = np.asarray(x, np.float64) @ np.asarray(weight, np.float64).T
+    return y if bias is None else y + np.asarray(bias, np.float64)
+
+
+def mha_forward(
+    x: np.ndarray,
+    key_value: np.ndarray | None,
+    weights: dict[str, np.ndarray],
+    num_heads: int,
+    num_kv_heads: int | None = None,
+    causal: bool = False,
+) -> np.ndarray:
+    """Module-level forward of ``MultiHeadAttention`` in float64.
+
+    Restates stratego/networks/attention.py:152-204: q/k/v projections from
+    ``x`` / ``key_value`` (:175-179), BSHD views (:184-186), causal masking only
+    for self-attention (:189), attention (:193-200), reshape and ``out_proj``
+    (:203-204).  ``weights`` holds the module's state_dict entries
+    (``q_proj.weight`` ... and optional ``*.bias``).
+    """
+    kv_heads = num_heads if num_kv_heads is None else num_kv_heads
+    src = x if key_value is None else key_value
+    b, s_q, e = x.shape
+    s_kv = src.shape[1]
+    d = e // num_heads
+    q = linear(x, weights["q_proj.weight"], weights.get("q_proj.bias")).reshape(b, s_q, num_heads, d)
+    k = linear(src, weights["k_proj.weight"], weights.get("k_proj.bias")).reshape(b, s_kv, kv_heads, d)
+    v = linear(src, weights["v_proj.weight"], weights.get("v_proj.bias")).reshape(b, s_kv, kv_heads, d)
+    o = attention(q, k, v, causal=causal and key_value is None)
+    return linear(o.reshape(b, s_q, num_heads * d), weights["out_proj.weight"], weights.get("out_proj.bias"))
