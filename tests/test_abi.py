@@ -1,0 +1,168 @@
+"""The C-ABI boundary, checked without a GPU.
+
+* the built library loads and exports every function ``include/*.h`` declares;
+* the ctypes structs have the C compiler's layout (sizeof / offsetof from a
+  probe compiled with gcc against the header);
+* host-side validation returns the documented codes and messages — these
+  calls return before any HIP call, so they run on a machine without a GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from ataraxos_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+STRUCTS = {"AtxAttnParams": _lib.AttnParams, "AtxKqParams": _lib.KqParams, "AtxDecodeParams": _lib.DecodeParams}
+
+
+def declared_functions() -> set[str]:
+    names = set()
+    for h in HEADERS:
+        text = h.read_text()
+        names |= set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(atx_\w+)\s*\(", text, flags=re.M))
+    return names
+
+
+def test_header_declares_the_bound_entry_points():
+    assert declared_functions() == set(_lib.ENTRY_POINTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.atx_abi_version() == _lib.ABI_VERSION
+
+
+def test_header_constants_match_bindings():
+    text = "".join(h.read_text() for h in HEADERS)
+    consts = dict(re.findall(r"#define\s+(ATX_\w+)\s+\(?(-?\d+)\)?", text))
+    assert int(consts["ATX_ABI_VERSION"]) == _lib.ABI_VERSION
+    for name, val in [("ATX_OK", _lib.OK), ("ATX_ERR_INVALID_ARGUMENT", _lib.ERR_INVALID_ARGUMENT),
+                      ("ATX_ERR_UNSUPPORTED", _lib.ERR_UNSUPPORTED), ("ATX_ERR_LAUNCH", _lib.ERR_LAUNCH),
+                      ("ATX_ERR_ABI", _lib.ERR_ABI), ("ATX_DTYPE_FP32", _lib.DTYPE_FP32),
+                      ("ATX_DTYPE_BF16", _lib.DTYPE_BF16), ("ATX_DTYPE_FP16", _lib.DTYPE_FP16),
+                      ("ATX_KQ_OUT_PROBS", _lib.KQ_OUT_PROBS), ("ATX_KQ_OUT_LOGITS", _lib.KQ_OUT_LOGITS)]:
+        assert int(consts[name]) == val, name
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_struct_layouts_match_c_compiler(tmp_path):
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "ataraxos_attn.h"', "int main(void) {"]
+    for cname, py in STRUCTS.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in py._fields_:
+            lines.append(f'  printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    for line in filter(None, out):
+        cname, field, value = line.split()
+        py = STRUCTS[cname]
+        want = ctypes.sizeof(py) if field == "size" else getattr(py, field).offset
+        assert int(value) == want, f"{cname}.{field}: C {value}, ctypes {want}"
+
+
+# --- validation without a GPU ------------------------------------------------
+
+
+def _attn_params(**kw) -> _lib.AttnParams:
+    p = _lib.AttnParams()
+    p.abi_version = _lib.ABI_VERSION
+    p.dtype = _lib.DTYPE_BF16
+    p.batch, p.seq_q, p.seq_kv, p.num_heads, p.num_kv_heads, p.head_dim = 2, 100, 100, 6, 6, 64
+    fake = 1 << 20  # never dereferenced: every case below fails validation first
+    p.q = p.k = p.v = p.o = fake
+    p.q_stride_b = p.k_stride_b = p.v_stride_b = p.o_stride_b = 100 * 384
+    p.q_stride_s = p.k_stride_s = p.v_stride_s = p.o_stride_s = 384
+    p.q_stride_h = p.k_stride_h = p.v_stride_h = p.o_stride_h = 64
+    p.scale = 0.125
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def _expect(name, params, code, text):
+    rc = _lib.call(name, params, None)
+    assert rc == code, (rc, _lib.last_error())
+    assert text in _lib.last_error()
+
+
+def test_attention_validation_codes():
+    lib = _lib.load()
+    assert lib.atx_attn_fwd(None, None) == _lib.ERR_INVALID_ARGUMENT
+    _expect("atx_attn_fwd", _attn_params(abi_version=99), _lib.ERR_ABI, "abi_version")
+    _expect("atx_attn_fwd", _attn_params(dtype=7), _lib.ERR_INVALID_ARGUMENT, "dtype")
+    _expect("atx_attn_fwd", _attn_params(batch=0), _lib.ERR_INVALID_ARGUMENT, "sizes")
+    _expect("atx_attn_fwd", _attn_params(num_kv_heads=4), _lib.ERR_INVALID_ARGUMENT, "divisible")
+    _expect("atx_attn_fwd", _attn_params(q=None), _lib.ERR_INVALID_ARGUMENT, "null")
+    _expect("atx_attn_fwd", _attn_params(scale=0.0), _lib.ERR_INVALID_ARGUMENT, "scale")
+    _expect("atx_attn_fwd", _attn_params(scale=float("nan")), _lib.ERR_INVALID_ARGUMENT, "scale")
+    _expect("atx_attn_fwd", _attn_params(head_dim=8), _lib.ERR_UNSUPPORTED, "head_dim")
+    _expect("atx_attn_fwd", _attn_params(head_dim=136), _lib.ERR_UNSUPPORTED, "head_dim")
+    _expect("atx_attn_fwd", _attn_params(seq_kv=257), _lib.ERR_UNSUPPORTED, "seq_kv")
+    _expect("atx_attn_fwd", _attn_params(q=(1 << 20) + 8), _lib.ERR_INVALID_ARGUMENT, "16-byte")
+    _expect("atx_attn_fwd", _attn_params(k_stride_s=385), _lib.ERR_INVALID_ARGUMENT, "16-byte")
+
+
+def test_policy_validation_codes():
+    p = _lib.KqParams()
+    p.abi_version, p.dtype, p.batch, p.seq, p.dim = _lib.ABI_VERSION, _lib.DTYPE_BF16, 4, 100, 64
+    p.q = p.k = p.out = 1 << 20
+    p.q_stride_b = p.k_stride_b = 6400
+    p.q_stride_s = p.k_stride_s = 64
+    p.out_stride_b = 10000
+    p.scale = 0.125
+    for field, value, code, text in [
+        ("out_mode", 5, _lib.ERR_INVALID_ARGUMENT, "out_mode"),
+        ("seq", 129, _lib.ERR_UNSUPPORTED, "seq"),
+        ("dim", 12, _lib.ERR_UNSUPPORTED, "dim"),
+        ("scale", -1.0, _lib.ERR_INVALID_ARGUMENT, "scale"),
+        ("out_stride_b", 9999, _lib.ERR_INVALID_ARGUMENT, "stride"),
+    ]:
+        saved = getattr(p, field)
+        setattr(p, field, value)
+        _expect("atx_kq_masked_softmax_fwd", p, code, text)
+        setattr(p, field, saved)
+
+
+def test_decode_validation_codes():
+    p = _lib.DecodeParams()
+    p.abi_version, p.dtype, p.batch, p.num_heads, p.num_kv_heads, p.head_dim = _lib.ABI_VERSION, _lib.DTYPE_BF16, 4, 8, 8, 64
+    p.kv_capacity, p.kv_len = 40, 41
+    p.q = p.k_cache = p.v_cache = p.o = 1 << 20
+    p.scale = 0.125
+    _expect("atx_attn_decode_fwd", p, _lib.ERR_INVALID_ARGUMENT, "kv_len")
+    p.kv_len = 10
+    p.k_new = 1 << 20
+    _expect("atx_attn_decode_fwd", p, _lib.ERR_INVALID_ARGUMENT, "together")
+    p.k_new = None
+    p.head_dim = 12
+    _expect("atx_attn_decode_fwd", p, _lib.ERR_UNSUPPORTED, "multiple")
+
+
+def test_error_text_is_per_call():
+    _expect("atx_attn_fwd", _attn_params(head_dim=8), _lib.ERR_UNSUPPORTED, "head_dim")
+    _expect("atx_attn_fwd", _attn_params(dtype=9), _lib.ERR_INVALID_ARGUMENT, "dtype")
+    assert "head_dim" not in _lib.last_error()
+
+
+def test_missing_library_raises_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setenv("ATARAXOS_AMD_LIB", str(tmp_path / "absent.so"))
+    with pytest.raises(_lib.AtxError, match="not found"):
+        _lib.load()
+    assert not _lib.available()
