@@ -67,24 +67,31 @@ __device__ inline uint64_t key_valid_bits(const AttnArgs& a, int b, int g, int n
     return bits;
 }
 
-// Waves per SIMD that the register allocator is asked to fit, per head_dim
-// (rows: 16, 32, 48, 64, 80, 96, 112, 128) and 32-key chunk count (columns:
-// NKC = 1..8).  Each entry is the highest target for which hipcc (ROCm 7.2,
-// gfx950) produced the kernel without register spills; the AMDGPU scheduler
+// Waves per SIMD that the register allocator is asked to fit, per kernel
+// family (16-bit plain / masked, fp32), head_dim (rows: 16, 32, 48, 64, 80,
+// 96, 112, 128) and 32-key chunk count (columns: NKC = 1..8).  Each entry is
+// the highest target for which hipcc (ROCm 7.2, gfx950) produced the kernel
+// (bf16 and fp16) without register spills; the AMDGPU scheduler
 // is not monotonic in this target (a looser budget can make it hoist loads
 // far enough to spill), so the values were found by compiling every
 // instantiation at every target, not by a formula.
-constexpr int kOcc16[8][8] = {
-    {8, 7, 8, 7, 5, 5, 4, 4}, {8, 7, 8, 7, 5, 5, 4, 4}, {8, 6, 8, 6, 5, 4, 4, 4}, {8, 7, 8, 6, 5, 4, 4, 4},
-    {8, 6, 7, 5, 5, 4, 4, 4}, {8, 6, 3, 5, 5, 4, 3, 3}, {7, 6, 3, 5, 4, 3, 3, 2}, {6, 5, 3, 3, 4, 3, 3, 2},
+constexpr int kOcc16[2][8][8] = {
+    {
+        {8, 8, 8, 8, 6, 5, 4, 4}, {8, 8, 8, 8, 6, 5, 4, 4}, {8, 8, 8, 7, 6, 4, 4, 4}, {8, 8, 8, 7, 5, 5, 4, 4},
+        {7, 7, 6, 5, 5, 4, 4, 3}, {6, 7, 6, 5, 4, 4, 3, 3}, {6, 5, 5, 4, 4, 3, 3, 2}, {5, 5, 5, 4, 4, 3, 3, 2},
+    },
+    {
+        {8, 8, 6, 5, 4, 3, 3, 2}, {8, 8, 6, 5, 4, 3, 3, 2}, {8, 8, 8, 5, 4, 4, 3, 3}, {8, 8, 7, 4, 4, 3, 3, 2},
+        {7, 7, 6, 6, 4, 4, 3, 3}, {7, 6, 6, 5, 4, 4, 3, 3}, {6, 5, 5, 5, 4, 3, 3, 2}, {5, 5, 5, 4, 4, 3, 3, 2},
+    },
 };
 constexpr int kOcc32[8][8] = {
-    {8, 8, 7, 5, 4, 4, 3, 3}, {8, 8, 6, 5, 4, 4, 3, 3}, {8, 7, 5, 4, 4, 3, 3, 3}, {8, 7, 5, 4, 4, 3, 3, 2},
-    {8, 7, 5, 4, 4, 3, 3, 2}, {8, 6, 5, 4, 4, 3, 3, 2}, {8, 6, 4, 4, 3, 3, 3, 2}, {7, 5, 4, 4, 3, 3, 3, 2},
+    {8, 8, 7, 5, 4, 4, 3, 3}, {8, 8, 6, 4, 4, 4, 3, 3}, {8, 7, 5, 4, 4, 3, 3, 3}, {8, 7, 5, 4, 4, 3, 3, 2},
+    {8, 6, 5, 4, 4, 3, 3, 2}, {8, 6, 5, 4, 3, 3, 3, 2}, {7, 5, 4, 4, 3, 3, 3, 2}, {7, 5, 4, 4, 3, 3, 2, 2},
 };
-template <int D, int NKC>
+template <int D, int NKC, bool MASKED>
 constexpr int occ_16bit() {
-    return kOcc16[D / 16 - 1][NKC - 1];
+    return kOcc16[MASKED ? 1 : 0][D / 16 - 1][NKC - 1];
 }
 template <int D, int NKC>
 constexpr int occ_fp32() {
@@ -92,24 +99,27 @@ constexpr int occ_fp32() {
 }
 
 // ---------------------------------------------------------------------------
-// 16-bit inputs (bf16 / fp16): NKC = number of 32-key chunks (S_kv <= 32*NKC).
+// 16-bit inputs (bf16 / fp16).  NKC = number of 32-key chunks (S_kv <= 32*NKC);
+// MASKED selects the variant with causal / key-padding masks, so the plain
+// kernel carries no per-element mask work beyond the key bound of its last
+// tile.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int NKC>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(occ_16bit<D, NKC>(), 8)))
+template <typename T, int D, int NKC, bool MASKED>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(occ_16bit<D, NKC, MASKED>(), 8)))
 void attn_fwd_16bit(AttnArgs a) {
     using M = Mfma16<T>;
     constexpr int CH = D / 8;          // 16-byte chunks per row
     constexpr int NI = (D + 31) / 32;  // QK^T MFMAs per 16x16 tile
     constexpr int NDT = D / 16;        // PV output tiles
     constexpr int QD = D / 4;          // contiguous outputs per lane
-    constexpr int RS = D * 2 + 16;     // K row stride in LDS (bytes)
-    constexpr int NB = (4 * NKC <= 16) ? 16 : 32;  // 16-byte blocks per V^T row
-    constexpr int RSV = NB * 16;
+    constexpr int RSK = D * 2 + 16;    // K row stride in LDS (bytes)
+    constexpr int RSV = D * 2;         // V row stride in LDS (bytes, 8-byte units swizzled)
     constexpr int NKT = 2 * NKC;
+    constexpr int VROWS = 32 * NKC;    // V rows staged (rows >= S_kv are zero)
 
     const int nkt = a.nkt;  // 2*NKC or 2*NKC - 1
     lds_t* const sk = lds_base();
-    lds_t* const svt = sk + nkt * 16 * RS;
+    lds_t* const sv = sk + nkt * 16 * RSK;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -117,6 +127,7 @@ void attn_fwd_16bit(AttnArgs a) {
     const int bh = blockIdx.x;
     const int b = bh / a.H, h = bh - b * a.H;
     const int hk = h / a.group;
+    const int qss = (int)a.qss, kss = (int)a.kss, vss = (int)a.vss, oss = (int)a.oss;
 
     const T* kb = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
     const T* vb = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
@@ -125,19 +136,19 @@ void attn_fwd_16bit(AttnArgs a) {
 
     const int nqt = (a.Sq + 15) >> 4;
 
-    // Q operand of this wave's first tile, issued before the staging loads.
+    // Q operand (B of S^T = K Q^T): lane (m, g) holds chunk 4i+g of query row m.
     auto load_q = [&](int qt, u32x4 (&qop)[NI]) {
         const int qrow = qt * 16 + m;
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int c = 4 * i + g;
-            qop[i] = (qrow < a.Sq && c < CH) ? ld16(qb + qrow * a.qss + c * 8) : u32x4{0, 0, 0, 0};
+            qop[i] = (qrow < a.Sq && c < CH) ? ld16(qb + qrow * qss + c * 8) : u32x4{0, 0, 0, 0};
         }
     };
     u32x4 qop[NI];
     if (wave < nqt) load_q(wave, qop);
 
-    // ---- stage K (row-major, padded rows) --------------------------------
+    // ---- stage K (row-major, rows padded to an odd number of 16B units) ---
     constexpr int KIT = (NKT * 16 * CH + kThreads - 1) / kThreads;
     u32x4 kreg[KIT];
     const int kchunks = a.Skv * CH;
@@ -145,76 +156,69 @@ void attn_fwd_16bit(AttnArgs a) {
     for (int it = 0; it < KIT; ++it) {
         const int idx = tid + it * kThreads;
         if (idx < kchunks) {
-            const int r = idx / CH, c = idx - (idx / CH) * CH;
-            kreg[it] = ld16(kb + r * a.kss + c * 8);
+            const int r = idx / CH, c = idx - r * CH;
+            kreg[it] = ld16(kb + r * kss + c * 8);
         }
     }
-    // ---- stage V^T: task = (4-key quad, 8-wide d chunk) ------------------
-    constexpr int VT = 8 * NKC * CH;
-    constexpr int VIT = (VT + kThreads - 1) / kThreads;
-    u32x4 vreg[VIT][4];
+    // ---- stage V (row-major; rows past S_kv are zero) ----------------------
+    constexpr int VIT = (VROWS * CH + kThreads - 1) / kThreads;
+    u32x4 vreg[VIT];
 #pragma unroll
     for (int it = 0; it < VIT; ++it) {
-        const int t = tid + it * kThreads;
-        const int dc = t % CH, kq = t / CH;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int key = 4 * kq + j;
-            vreg[it][j] = (t < VT && key < a.Skv) ? ld16(vb + key * a.vss + dc * 8) : u32x4{0, 0, 0, 0};
-        }
+        const int idx = tid + it * kThreads;
+        const int r = idx / CH, c = idx - r * CH;
+        vreg[it] = (idx < VROWS * CH && r < a.Skv) ? ld16(vb + r * vss + c * 8) : u32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int it = 0; it < KIT; ++it) {
         const int idx = tid + it * kThreads;
         if (idx < kchunks) {
-            const int r = idx / CH, c = idx - (idx / CH) * CH;
-            lds_st16(sk + r * RS + c * 16, kreg[it]);
+            const int r = idx / CH, c = idx - r * CH;
+            lds_st16(sk + r * RSK + c * 16, kreg[it]);
         }
     }
+    // The 8-byte units of V row r sit at unit ^ s(r), s(r) = ((r >> 1) ^ r) & 3:
+    // the transposing reads below then touch 32 distinct bank pairs per phase.
 #pragma unroll
     for (int it = 0; it < VIT; ++it) {
-        const int t = tid + it * kThreads;
-        if (t < VT) {
-            const int dc = t % CH, kq = t / CH;
-            const int key0 = 4 * kq;
-            const int w = key0 & 31;
-            const int lb = 4 * (key0 >> 5) + ((w & 15) >> 2);  // logical block
-            const int boff = (w >> 4) * 8;                      // byte offset in block
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t x0 = vreg[it][0][e], x1 = vreg[it][1][e];
-                const uint32_t x2 = vreg[it][2][e], x3 = vreg[it][3][e];
-                const u32x2 even = {(x0 & 0xffffu) | (x1 << 16), (x2 & 0xffffu) | (x3 << 16)};
-                const u32x2 odd = {(x0 >> 16) | (x1 & 0xffff0000u), (x2 >> 16) | (x3 & 0xffff0000u)};
-                const int d0 = dc * 8 + 2 * e, d1 = d0 + 1;
-                const int h0 = ((d0 / QD) << 2) | (d0 & 3), h1 = ((d1 / QD) << 2) | (d1 & 3);
-                lds_st8(svt + d0 * RSV + ((lb ^ h0) << 4) + boff, even);
-                lds_st8(svt + d1 * RSV + ((lb ^ h1) << 4) + boff, odd);
-            }
+        const int idx = tid + it * kThreads;
+        if (idx < VROWS * CH) {
+            const int r = idx / CH, c = idx - r * CH;
+            const int sw = ((r >> 1) ^ r) & 3;
+            lds_t* row = sv + r * RSV;
+            lds_st8(row + (((2 * c) ^ sw) << 3), u32x2{vreg[it][0], vreg[it][1]});
+            lds_st8(row + (((2 * c + 1) ^ sw) << 3), u32x2{vreg[it][2], vreg[it][3]});
         }
     }
 
-    const bool masked_path = a.causal || a.kpad != nullptr;
     uint64_t kbits = 0;
-    if (masked_path) kbits = key_valid_bits(a, b, g, nkt);
+    if constexpr (MASKED) kbits = key_valid_bits(a, b, g, nkt);
     const bool last_full = (nkt == NKT);
     __syncthreads();
 
     const float c2 = a.c2;
     const float kNegInf = -__builtin_inff();
+    // Transposing-read geometry of this lane (ds_read_b64_tr_b16): input lane
+    // i = a4 + 4t of a 16-lane group points at row 4g + t (+32c + 16h) and
+    // columns a4*QD + 4dt..+3; the read hands lane m the four keys of its
+    // group for head-dim (m/4)*QD + 4dt + m%4.
+    const int tr_t = m >> 2, tr_a = m & 3;
+    const int tr_row = 4 * g + tr_t;
+    const int tr_sw = ((tr_row >> 1) ^ tr_row) & 3;
+    const uint32_t ones = M::kOnes2;
 
     for (int qt = wave; qt < nqt; qt += kWaves) {
         const int qrow = qt * 16 + m;
         lds_t* const skq = lds_opaque(sk);
-        lds_t* const svq = lds_opaque(svt);
+        lds_t* const svq = lds_opaque(sv);
 
-        // ---- S^T = K Q^T over the key tiles -----------------------------
+        // ---- S^T = K Q^T over the key tiles -------------------------------
         f32x4 s[NKT];
 #pragma unroll
         for (int kt = 0; kt < NKT; ++kt) {
             s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
             if (kt < NKT - 1 || last_full) {
-                const lds_t* krow = skq + (kt * 16 + m) * RS;
+                const lds_t* krow = skq + (kt * 16 + m) * RSK;
 #pragma unroll
                 for (int i = 0; i < NI; ++i) {
                     const int c = 4 * i + g;
@@ -224,17 +228,14 @@ void attn_fwd_16bit(AttnArgs a) {
                 }
             }
         }
-        // Prefetch the next tile's Q operand while the softmax runs.
         if (qt + kWaves < nqt) load_q(qt + kWaves, qop);
-        // Phase fences: keep the scheduler from hoisting the PV operand reads
-        // above the softmax, which would hold both phases' registers at once.
+        // Phase fence: keeps the PV operand reads below the softmax.
         __builtin_amdgcn_sched_barrier(0);
 
-        // ---- mask ---------------------------------------------------------
+        // ---- mask -----------------------------------------------------------
 #pragma unroll
         for (int kt = 0; kt < NKT; ++kt) {
-            const bool partial = (kt * 16 + 16 > a.Skv);
-            if (masked_path) {
+            if constexpr (MASKED) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int key = kt * 16 + 4 * g + i;
@@ -242,27 +243,25 @@ void attn_fwd_16bit(AttnArgs a) {
                     if (a.causal) ok = ok && key <= qrow;
                     s[kt][i] = ok ? s[kt][i] : kNegInf;
                 }
-            } else if (partial) {
+            } else if (kt * 16 + 16 > a.Skv) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int key = kt * 16 + 4 * g + i;
-                    s[kt][i] = key < a.Skv ? s[kt][i] : kNegInf;
-                }
+                for (int i = 0; i < 4; ++i) s[kt][i] = (kt * 16 + 4 * g + i < a.Skv) ? s[kt][i] : kNegInf;
             }
         }
 
-        // ---- single-pass softmax over the whole key row -------------------
+        // ---- single-pass softmax over the whole key row ---------------------
         float mx = kNegInf;
 #pragma unroll
-        for (int kt = 0; kt < NKT; ++kt)
+        for (int kt = 0; kt < NKT; ++kt) {
+            if (kt < NKT - 1 || last_full) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][i]);
+                for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][i]);
+            }
+        }
         mx = colgroup_max(mx);
         // A fully masked row has mx = -inf; -mb = +inf then makes every
         // exponent NaN, which is what softmax over an all -inf row returns.
         const float mb = mx * c2;
-
-        float lsum = 0.f;
         u32x4 pk[NKC];
 #pragma unroll
         for (int c = 0; c < NKC; ++c) {
@@ -271,37 +270,34 @@ void attn_fwd_16bit(AttnArgs a) {
             for (int hh = 0; hh < 2; ++hh) {
                 const int kt = 2 * c + hh;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float e = fast_exp2(__builtin_fmaf(s[kt][i], c2, -mb));
-                    if (kt == NKT - 1 && !last_full) e = 0.f;
-                    p[4 * hh + i] = e;
-                    lsum += e;
-                }
+                for (int i = 0; i < 4; ++i)
+                    p[4 * hh + i] = (kt < NKT - 1 || last_full) ? fast_exp2(__builtin_fmaf(s[kt][i], c2, -mb)) : 0.f;
             }
-            pk[c] = u32x4{M::pack2(p[0], p[1]), M::pack2(p[2], p[3]), M::pack2(p[4], p[5]),
-                          M::pack2(p[6], p[7])};
+            pk[c] = u32x4{M::pack2(p[0], p[1]), M::pack2(p[2], p[3]), M::pack2(p[4], p[5]), M::pack2(p[6], p[7])};
         }
-        lsum = colgroup_sum(lsum);
         __builtin_amdgcn_sched_barrier(0);
 
-        // ---- O^T = V^T P^T -----------------------------------------------
+        // ---- O^T = V^T P^T, and the row sums as ones^T P^T ------------------
+        f32x4 lsum4 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NKC; ++c) lsum4 = M::mma(u32x4{ones, ones, ones, ones}, pk[c], lsum4);
         f32x4 oacc[NDT];
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
             oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-            const int d = (m >> 2) * QD + dt * 4 + (m & 3);
-            const lds_t* vrow = svq + d * RSV;
+            const lds_t* vlane = svq + tr_row * RSV + ((((tr_a * NDT) + dt) ^ tr_sw) << 3);
 #pragma unroll
             for (int c = 0; c < NKC; ++c) {
-                const u32x4 vop = lds_ld16(vrow + (((4 * c + g) ^ m) << 4));
-                oacc[dt] = M::mma(vop, pk[c], oacc[dt]);
+                const u32x2 lo = lds_ld8_tr16(vlane + (32 * c) * RSV);
+                const u32x2 hi = lds_ld8_tr16(vlane + (32 * c + 16) * RSV);
+                oacc[dt] = M::mma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[c], oacc[dt]);
             }
         }
 
-        // ---- normalise and store D/4 contiguous outputs per lane ----------
+        // ---- normalise and store D/4 contiguous outputs per lane ------------
         if (qrow < a.Sq) {
-            const float inv = fast_rcp(lsum);
-            T* orow = ob + qrow * a.oss + g * QD;
+            const float inv = fast_rcp(lsum4[0]);
+            T* orow = ob + qrow * oss + g * QD;
             if constexpr (QD % 8 == 0) {
 #pragma unroll
                 for (int dt = 0; dt < NDT; dt += 2) {
@@ -488,22 +484,28 @@ int launch(Kernel kernel, int grid, size_t lds, hipStream_t stream, const AttnAr
     return ATX_OK;
 }
 
+template <typename T, int D, bool MASKED>
+int dispatch_16bit_mode(int nkc, int grid, size_t lds, hipStream_t st, const AttnArgs& a) {
+    switch (nkc) {
+        case 1: return launch(attn_fwd_16bit<T, D, 1, MASKED>, grid, lds, st, a);
+        case 2: return launch(attn_fwd_16bit<T, D, 2, MASKED>, grid, lds, st, a);
+        case 3: return launch(attn_fwd_16bit<T, D, 3, MASKED>, grid, lds, st, a);
+        case 4: return launch(attn_fwd_16bit<T, D, 4, MASKED>, grid, lds, st, a);
+        case 5: return launch(attn_fwd_16bit<T, D, 5, MASKED>, grid, lds, st, a);
+        case 6: return launch(attn_fwd_16bit<T, D, 6, MASKED>, grid, lds, st, a);
+        case 7: return launch(attn_fwd_16bit<T, D, 7, MASKED>, grid, lds, st, a);
+        case 8: return launch(attn_fwd_16bit<T, D, 8, MASKED>, grid, lds, st, a);
+    }
+    ATX_FAIL(ATX_ERR_UNSUPPORTED, "seq_kv chunk count %d", nkc);
+}
+
 template <typename T, int D>
 int dispatch_16bit(int nkc, int grid, hipStream_t st, const AttnArgs& a) {
     const size_t k_lds = (size_t)a.nkt * 16 * (D * 2 + 16);
-    const size_t vt_lds = (size_t)D * ((4 * nkc <= 16) ? 16 : 32) * 16;
-    const size_t lds = k_lds + vt_lds;
-    switch (nkc) {
-        case 1: return launch(attn_fwd_16bit<T, D, 1>, grid, lds, st, a);
-        case 2: return launch(attn_fwd_16bit<T, D, 2>, grid, lds, st, a);
-        case 3: return launch(attn_fwd_16bit<T, D, 3>, grid, lds, st, a);
-        case 4: return launch(attn_fwd_16bit<T, D, 4>, grid, lds, st, a);
-        case 5: return launch(attn_fwd_16bit<T, D, 5>, grid, lds, st, a);
-        case 6: return launch(attn_fwd_16bit<T, D, 6>, grid, lds, st, a);
-        case 7: return launch(attn_fwd_16bit<T, D, 7>, grid, lds, st, a);
-        case 8: return launch(attn_fwd_16bit<T, D, 8>, grid, lds, st, a);
-    }
-    ATX_FAIL(ATX_ERR_UNSUPPORTED, "seq_kv chunk count %d", nkc);
+    const size_t v_lds = (size_t)32 * nkc * D * 2;
+    const size_t lds = k_lds + v_lds;
+    if (a.causal || a.kpad) return dispatch_16bit_mode<T, D, true>(nkc, grid, lds, st, a);
+    return dispatch_16bit_mode<T, D, false>(nkc, grid, lds, st, a);
 }
 
 template <int D>

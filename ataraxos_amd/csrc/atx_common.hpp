@@ -50,6 +50,7 @@ struct Mfma16;
 template <>
 struct Mfma16<__bf16> {
     static constexpr int kDtype = ATX_DTYPE_BF16;
+    static constexpr uint32_t kOnes2 = 0x3F803F80u;  // two packed 1.0
     __device__ static inline f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -70,6 +71,7 @@ struct Mfma16<__bf16> {
 template <>
 struct Mfma16<_Float16> {
     static constexpr int kDtype = ATX_DTYPE_FP16;
+    static constexpr uint32_t kOnes2 = 0x3C003C00u;  // two packed 1.0
     __device__ static inline f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
@@ -136,6 +138,14 @@ __device__ inline lds_t* lds_opaque(lds_t* p) {
 
 __device__ inline u32x4 lds_ld16(const lds_t* p) { return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(p); }
 __device__ inline void lds_st16(lds_t* p, u32x4 v) { *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(p) = v; }
+// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element j%4
+// of the 8-byte rows addressed by lanes j/4, j/4+4, j/4+8, j/4+12.
+__device__ inline u32x2 lds_ld8_tr16(const lds_t* p) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(p));
+    return __builtin_bit_cast(u32x2, v);
+}
 __device__ inline void lds_st8(lds_t* p, u32x2 v) { *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(p) = v; }
 
 // 16-byte global load / store through the vector memory path.
