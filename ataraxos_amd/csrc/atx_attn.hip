@@ -77,17 +77,35 @@ __device__ inline uint64_t key_valid_bits(const AttnArgs& a, int b, int g, int n
 // instantiation at every target, not by a formula.
 constexpr int kOcc16[2][8][8] = {
     {
-        {8, 8, 8, 8, 6, 5, 4, 4}, {8, 8, 8, 8, 6, 5, 4, 4}, {8, 8, 8, 7, 6, 4, 4, 4}, {8, 8, 8, 7, 5, 5, 4, 4},
-        {7, 7, 6, 5, 5, 4, 4, 3}, {6, 7, 6, 5, 4, 4, 3, 3}, {6, 5, 5, 4, 4, 3, 3, 2}, {5, 5, 5, 4, 4, 3, 3, 2},
+        {8, 8, 8, 8, 7, 6, 5, 5},
+        {8, 8, 8, 7, 6, 5, 5, 4},
+        {8, 8, 7, 6, 5, 5, 4, 4},
+        {8, 7, 7, 6, 5, 5, 4, 4},
+        {7, 6, 6, 5, 5, 4, 4, 4},
+        {6, 6, 5, 5, 4, 4, 3, 3},
+        {5, 5, 5, 4, 4, 3, 3, 3},
+        {5, 5, 4, 4, 4, 3, 3, 2},
     },
     {
-        {8, 8, 6, 5, 4, 3, 3, 2}, {8, 8, 6, 5, 4, 3, 3, 2}, {8, 8, 8, 5, 4, 4, 3, 3}, {8, 8, 7, 4, 4, 3, 3, 2},
-        {7, 7, 6, 6, 4, 4, 3, 3}, {7, 6, 6, 5, 4, 4, 3, 3}, {6, 5, 5, 5, 4, 3, 3, 2}, {5, 5, 5, 4, 4, 3, 3, 2},
+        {8, 8, 7, 5, 4, 3, 3, 2},
+        {8, 8, 6, 5, 4, 3, 3, 2},
+        {8, 8, 7, 5, 4, 4, 3, 3},
+        {8, 8, 8, 7, 4, 4, 3, 3},
+        {8, 7, 7, 6, 4, 4, 3, 3},
+        {7, 7, 6, 6, 4, 4, 3, 3},
+        {6, 5, 5, 5, 4, 3, 3, 2},
+        {5, 5, 5, 4, 4, 3, 3, 2},
     },
 };
 constexpr int kOcc32[8][8] = {
-    {8, 8, 7, 5, 4, 4, 3, 3}, {8, 8, 6, 4, 4, 4, 3, 3}, {8, 7, 5, 4, 4, 3, 3, 3}, {8, 7, 5, 4, 4, 3, 3, 2},
-    {8, 6, 5, 4, 4, 3, 3, 2}, {8, 6, 5, 4, 3, 3, 3, 2}, {7, 5, 4, 4, 3, 3, 3, 2}, {7, 5, 4, 4, 3, 3, 2, 2},
+    {8, 8, 7, 5, 4, 4, 3, 3},
+    {8, 8, 6, 4, 4, 4, 3, 3},
+    {8, 7, 5, 4, 4, 3, 3, 3},
+    {8, 7, 5, 4, 4, 3, 3, 2},
+    {8, 6, 5, 4, 4, 3, 3, 2},
+    {8, 6, 5, 4, 3, 3, 3, 2},
+    {7, 5, 4, 4, 3, 3, 3, 2},
+    {7, 5, 4, 4, 3, 3, 2, 2},
 };
 template <int D, int NKC, bool MASKED>
 constexpr int occ_16bit() {
@@ -148,17 +166,16 @@ void attn_fwd_16bit(AttnArgs a) {
     u32x4 qop[NI];
     if (wave < nqt) load_q(wave, qop);
 
-    // ---- stage K (row-major, rows padded to an odd number of 16B units) ---
+    // ---- stage K (row-major, rows padded to an odd number of 16B units;
+    //      rows from S_kv up to the last tile are zero) ---------------------
     constexpr int KIT = (NKT * 16 * CH + kThreads - 1) / kThreads;
     u32x4 kreg[KIT];
-    const int kchunks = a.Skv * CH;
+    const int kchunks = nkt * 16 * CH;
 #pragma unroll
     for (int it = 0; it < KIT; ++it) {
         const int idx = tid + it * kThreads;
-        if (idx < kchunks) {
-            const int r = idx / CH, c = idx - r * CH;
-            kreg[it] = ld16(kb + r * kss + c * 8);
-        }
+        const int r = idx / CH, c = idx - r * CH;
+        kreg[it] = (idx < kchunks && r < a.Skv) ? ld16(kb + r * kss + c * 8) : u32x4{0, 0, 0, 0};
     }
     // ---- stage V (row-major; rows past S_kv are zero) ----------------------
     constexpr int VIT = (VROWS * CH + kThreads - 1) / kThreads;
@@ -191,13 +208,20 @@ void attn_fwd_16bit(AttnArgs a) {
         }
     }
 
+    const float c2 = a.c2;
+    const float kNegInf = -__builtin_inff();
     uint64_t kbits = 0;
     if constexpr (MASKED) kbits = key_valid_bits(a, b, g, nkt);
     const bool last_full = (nkt == NKT);
+    // Keys at or past S_kv can only sit in the last two tiles (S_kv > 16*(NKT-2)):
+    // an additive 0 / -inf bias per lane masks them with one add per score.
+    float kbias[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kbias[j][i] = ((NKT - 2 + j) * 16 + 4 * g + i < a.Skv) ? 0.f : kNegInf;
     __syncthreads();
 
-    const float c2 = a.c2;
-    const float kNegInf = -__builtin_inff();
     // Transposing-read geometry of this lane (ds_read_b64_tr_b16): input lane
     // i = a4 + 4t of a 16-lane group points at row 4g + t (+32c + 16h) and
     // columns a4*QD + 4dt..+3; the read hands lane m the four keys of its
@@ -214,19 +238,26 @@ void attn_fwd_16bit(AttnArgs a) {
 
         // ---- S^T = K Q^T over the key tiles -------------------------------
         f32x4 s[NKT];
+        auto tile_scores = [&](int kt) {
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+            const lds_t* krow = skq + (kt * 16 + m) * RSK;
 #pragma unroll
-        for (int kt = 0; kt < NKT; ++kt) {
-            s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (kt < NKT - 1 || last_full) {
-                const lds_t* krow = skq + (kt * 16 + m) * RSK;
-#pragma unroll
-                for (int i = 0; i < NI; ++i) {
-                    const int c = 4 * i + g;
-                    u32x4 kop = lds_ld16(krow + c * 16);
-                    if (CH % 4 != 0 && c >= CH) kop = u32x4{0, 0, 0, 0};
-                    s[kt] = M::mma(kop, qop[i], s[kt]);
-                }
+            for (int i = 0; i < NI; ++i) {
+                const int c = 4 * i + g;
+                u32x4 kop = lds_ld16(krow + c * 16);
+                if (CH % 4 != 0 && c >= CH) kop = u32x4{0, 0, 0, 0};
+                acc = M::mma(kop, qop[i], acc);
             }
+            return acc;
+        };
+#pragma unroll
+        for (int kt = 0; kt < NKT - 1; ++kt) s[kt] = tile_scores(kt);
+        // The last tile exists only when S_kv > 16*(NKT-1); otherwise its
+        // scores are -inf and its probabilities come out as exp2(-inf) = 0.
+        if (last_full) {
+            s[NKT - 1] = tile_scores(NKT - 1);
+        } else {
+            s[NKT - 1] = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
         }
         if (qt + kWaves < nqt) load_q(qt + kWaves, qop);
         // Phase fence: keeps the PV operand reads below the softmax.
@@ -243,21 +274,18 @@ void attn_fwd_16bit(AttnArgs a) {
                     if (a.causal) ok = ok && key <= qrow;
                     s[kt][i] = ok ? s[kt][i] : kNegInf;
                 }
-            } else if (kt * 16 + 16 > a.Skv) {
+            } else if (kt >= NKT - 2) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) s[kt][i] = (kt * 16 + 4 * g + i < a.Skv) ? s[kt][i] : kNegInf;
+                for (int i = 0; i < 4; ++i) s[kt][i] += kbias[kt - (NKT - 2)][i];
             }
         }
 
         // ---- single-pass softmax over the whole key row ---------------------
         float mx = kNegInf;
 #pragma unroll
-        for (int kt = 0; kt < NKT; ++kt) {
-            if (kt < NKT - 1 || last_full) {
+        for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][i]);
-            }
-        }
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kt][i]);
         mx = colgroup_max(mx);
         // A fully masked row has mx = -inf; -mb = +inf then makes every
         // exponent NaN, which is what softmax over an all -inf row returns.
@@ -270,8 +298,7 @@ void attn_fwd_16bit(AttnArgs a) {
             for (int hh = 0; hh < 2; ++hh) {
                 const int kt = 2 * c + hh;
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    p[4 * hh + i] = (kt < NKT - 1 || last_full) ? fast_exp2(__builtin_fmaf(s[kt][i], c2, -mb)) : 0.f;
+                for (int i = 0; i < 4; ++i) p[4 * hh + i] = fast_exp2(__builtin_fmaf(s[kt][i], c2, -mb));
             }
             pk[c] = u32x4{M::pack2(p[0], p[1]), M::pack2(p[2], p[3]), M::pack2(p[4], p[5]), M::pack2(p[6], p[7])};
         }
