@@ -77,24 +77,24 @@ __device__ inline uint64_t key_valid_bits(const AttnArgs& a, int b, int g, int n
 // instantiation at every target, not by a formula.
 constexpr int kOcc16[2][8][8] = {
     {
-        {8, 8, 8, 8, 7, 6, 5, 5},
+        {8, 8, 8, 7, 6, 5, 5, 4},
         {8, 8, 8, 7, 6, 5, 5, 4},
         {8, 8, 7, 6, 5, 5, 4, 4},
-        {8, 7, 7, 6, 5, 5, 4, 4},
+        {6, 6, 5, 5, 5, 4, 4, 4},
         {7, 6, 6, 5, 5, 4, 4, 4},
         {6, 6, 5, 5, 4, 4, 3, 3},
         {5, 5, 5, 4, 4, 3, 3, 3},
-        {5, 5, 4, 4, 4, 3, 3, 2},
+        {4, 4, 4, 4, 4, 3, 3, 3},
     },
     {
-        {8, 8, 7, 5, 4, 3, 3, 2},
         {8, 8, 6, 5, 4, 3, 3, 2},
-        {8, 8, 7, 5, 4, 4, 3, 3},
-        {8, 8, 8, 7, 4, 4, 3, 3},
-        {8, 7, 7, 6, 4, 4, 3, 3},
-        {7, 7, 6, 6, 4, 4, 3, 3},
-        {6, 5, 5, 5, 4, 3, 3, 2},
-        {5, 5, 5, 4, 4, 3, 3, 2},
+        {8, 8, 8, 5, 4, 3, 3, 2},
+        {8, 8, 5, 5, 4, 3, 3, 3},
+        {8, 7, 6, 4, 4, 3, 3, 2},
+        {8, 7, 6, 6, 4, 4, 3, 3},
+        {7, 6, 5, 5, 4, 4, 3, 3},
+        {6, 5, 4, 5, 4, 3, 3, 3},
+        {5, 4, 4, 4, 4, 3, 3, 2},
     },
 };
 constexpr int kOcc32[8][8] = {
@@ -116,6 +116,18 @@ constexpr int occ_fp32() {
     return kOcc32[D / 16 - 1][NKC - 1];
 }
 
+// K rows: XOR-swizzled 16-byte chunks when a row has 8 or 16 of them, else
+// padded by one chunk.  Output stores go through LDS for D = 64 and 128
+// (rows of whole 128-byte lines).
+template <int D>
+constexpr bool kKeySwizzle = (D == 64 || D == 128);
+template <int D>
+constexpr int K_row_bytes() {
+    return kKeySwizzle<D> ? D * 2 : D * 2 + 16;
+}
+template <int D>
+constexpr bool kStagedStores = (D == 64 || D == 128);
+
 // ---------------------------------------------------------------------------
 // 16-bit inputs (bf16 / fp16).  NKC = number of 32-key chunks (S_kv <= 32*NKC);
 // MASKED selects the variant with causal / key-padding masks, so the plain
@@ -130,14 +142,17 @@ void attn_fwd_16bit(AttnArgs a) {
     constexpr int NI = (D + 31) / 32;  // QK^T MFMAs per 16x16 tile
     constexpr int NDT = D / 16;        // PV output tiles
     constexpr int QD = D / 4;          // contiguous outputs per lane
-    constexpr int RSK = D * 2 + 16;    // K row stride in LDS (bytes)
-    constexpr int RSV = D * 2;         // V row stride in LDS (bytes, 8-byte units swizzled)
     constexpr int NKT = 2 * NKC;
-    constexpr int VROWS = 32 * NKC;    // V rows staged (rows >= S_kv are zero)
+    constexpr bool KSWZ = kKeySwizzle<D>;   // K rows XOR-swizzled instead of padded
+    constexpr int RSK = K_row_bytes<D>();   // K row stride in LDS (bytes)
+    constexpr int RSV = D * 2;              // V row stride in LDS (bytes, 8-byte units swizzled)
+    constexpr bool STAGE_OUT = kStagedStores<D>;  // whole-line output stores through LDS
+    constexpr int OROWS = 8;                // output rows staged per round
 
     const int nkt = a.nkt;  // 2*NKC or 2*NKC - 1
     lds_t* const sk = lds_base();
     lds_t* const sv = sk + nkt * 16 * RSK;
+    lds_t* const so = sv + nkt * 16 * RSV;  // per-wave output staging (STAGE_OUT)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -160,14 +175,17 @@ void attn_fwd_16bit(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int c = 4 * i + g;
-            qop[i] = (qrow < a.Sq && c < CH) ? ld16(qb + qrow * qss + c * 8) : u32x4{0, 0, 0, 0};
+            qop[i] = (qrow < a.Sq && c < CH) ? ld16_stream(qb + qrow * qss + c * 8) : u32x4{0, 0, 0, 0};
         }
     };
     u32x4 qop[NI];
     if (wave < nqt) load_q(wave, qop);
 
-    // ---- stage K (row-major, rows padded to an odd number of 16B units;
-    //      rows from S_kv up to the last tile are zero) ---------------------
+    // ---- stage K (row-major; rows from S_kv up to the last tile are zero).
+    //      With 8 or 16 chunks per row the 16-byte chunk c of row r sits at
+    //      c ^ ((r >> 1) & 7); otherwise rows are padded to an odd number of
+    //      16-byte units.  Either way the 16 rows of one MFMA operand read
+    //      fall in distinct bank groups. --------------------------------------
     constexpr int KIT = (NKT * 16 * CH + kThreads - 1) / kThreads;
     u32x4 kreg[KIT];
     const int kchunks = nkt * 16 * CH;
@@ -175,23 +193,24 @@ void attn_fwd_16bit(AttnArgs a) {
     for (int it = 0; it < KIT; ++it) {
         const int idx = tid + it * kThreads;
         const int r = idx / CH, c = idx - r * CH;
-        kreg[it] = (idx < kchunks && r < a.Skv) ? ld16(kb + r * kss + c * 8) : u32x4{0, 0, 0, 0};
+        kreg[it] = (idx < kchunks && r < a.Skv) ? ld16_stream(kb + r * kss + c * 8) : u32x4{0, 0, 0, 0};
     }
-    // ---- stage V (row-major; rows past S_kv are zero) ----------------------
-    constexpr int VIT = (VROWS * CH + kThreads - 1) / kThreads;
+    // ---- stage V (row-major, rows up to the last tile; rows past S_kv zero)
+    constexpr int VIT = KIT;
     u32x4 vreg[VIT];
 #pragma unroll
     for (int it = 0; it < VIT; ++it) {
         const int idx = tid + it * kThreads;
         const int r = idx / CH, c = idx - r * CH;
-        vreg[it] = (idx < VROWS * CH && r < a.Skv) ? ld16(vb + r * vss + c * 8) : u32x4{0, 0, 0, 0};
+        vreg[it] = (idx < kchunks && r < a.Skv) ? ld16_stream(vb + r * vss + c * 8) : u32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int it = 0; it < KIT; ++it) {
         const int idx = tid + it * kThreads;
         if (idx < kchunks) {
             const int r = idx / CH, c = idx - r * CH;
-            lds_st16(sk + r * RSK + c * 16, kreg[it]);
+            const int pc = KSWZ ? (c ^ ((r >> 1) & 7)) : c;
+            lds_st16(sk + r * RSK + pc * 16, kreg[it]);
         }
     }
     // The 8-byte units of V row r sit at unit ^ s(r), s(r) = ((r >> 1) ^ r) & 3:
@@ -199,7 +218,7 @@ void attn_fwd_16bit(AttnArgs a) {
 #pragma unroll
     for (int it = 0; it < VIT; ++it) {
         const int idx = tid + it * kThreads;
-        if (idx < VROWS * CH) {
+        if (idx < kchunks) {
             const int r = idx / CH, c = idx - r * CH;
             const int sw = ((r >> 1) ^ r) & 3;
             lds_t* row = sv + r * RSV;
@@ -244,7 +263,9 @@ void attn_fwd_16bit(AttnArgs a) {
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 const int c = 4 * i + g;
-                u32x4 kop = lds_ld16(krow + c * 16);
+                // (kt*16 + m) >> 1 has the same low three bits as m >> 1.
+                const int pc = KSWZ ? (c ^ ((m >> 1) & 7)) : c;
+                u32x4 kop = lds_ld16(krow + pc * 16);
                 if (CH % 4 != 0 && c >= CH) kop = u32x4{0, 0, 0, 0};
                 acc = M::mma(kop, qop[i], acc);
             }
@@ -316,14 +337,44 @@ void attn_fwd_16bit(AttnArgs a) {
 #pragma unroll
             for (int c = 0; c < NKC; ++c) {
                 const u32x2 lo = lds_ld8_tr16(vlane + (32 * c) * RSV);
-                const u32x2 hi = lds_ld8_tr16(vlane + (32 * c + 16) * RSV);
+                // V rows exist up to the last tile; a missing tile has P = 0.
+                u32x2 hi = u32x2{0u, 0u};
+                if (c < NKC - 1 || last_full) hi = lds_ld8_tr16(vlane + (32 * c + 16) * RSV);
                 oacc[dt] = M::mma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[c], oacc[dt]);
             }
         }
 
-        // ---- normalise and store D/4 contiguous outputs per lane ------------
-        if (qrow < a.Sq) {
-            const float inv = fast_rcp(lsum4[0]);
+        // ---- normalise; store D/4 contiguous outputs per lane, or (D = 64,
+        //      128) through a per-wave LDS tile so every store instruction
+        //      writes whole 128-byte rows with the streaming hint ------------
+        const float inv = fast_rcp(lsum4[0]);
+        if constexpr (STAGE_OUT) {
+            lds_t* const sow = lds_opaque(so) + wave * (OROWS * 2 * D);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if ((m >> 3) == j) {
+                    lds_t* dst = sow + (m & 7) * (2 * D) + g * (QD * 2);
+#pragma unroll
+                    for (int dt = 0; dt < NDT; dt += 2) {
+                        const u32x4 w = {M::pack2(oacc[dt][0] * inv, oacc[dt][1] * inv),
+                                         M::pack2(oacc[dt][2] * inv, oacc[dt][3] * inv),
+                                         M::pack2(oacc[dt + 1][0] * inv, oacc[dt + 1][1] * inv),
+                                         M::pack2(oacc[dt + 1][2] * inv, oacc[dt + 1][3] * inv)};
+                        lds_st16(dst + dt * 8, w);
+                    }
+                }
+                // LDS accesses of one wave complete in order: the reads see
+                // the writes above, and the next round's writes follow them.
+#pragma unroll
+                for (int k = 0; k < CH / 8; ++k) {
+                    const int idx = lane + 64 * k;
+                    const int row = idx / CH, c = idx - row * CH;
+                    const u32x4 w = lds_ld16(sow + row * (2 * D) + c * 16);
+                    const int orow_i = qt * 16 + OROWS * j + row;
+                    if (orow_i < a.Sq) st16_stream(ob + orow_i * oss + c * 8, w);
+                }
+            }
+        } else if (qrow < a.Sq) {
             T* orow = ob + qrow * oss + g * QD;
             if constexpr (QD % 8 == 0) {
 #pragma unroll
@@ -528,9 +579,10 @@ int dispatch_16bit_mode(int nkc, int grid, size_t lds, hipStream_t st, const Att
 
 template <typename T, int D>
 int dispatch_16bit(int nkc, int grid, hipStream_t st, const AttnArgs& a) {
-    const size_t k_lds = (size_t)a.nkt * 16 * (D * 2 + 16);
-    const size_t v_lds = (size_t)32 * nkc * D * 2;
-    const size_t lds = k_lds + v_lds;
+    const size_t k_lds = (size_t)a.nkt * 16 * K_row_bytes<D>();
+    const size_t v_lds = (size_t)a.nkt * 16 * D * 2;
+    const size_t o_lds = kStagedStores<D> ? (size_t)kWaves * 8 * D * 2 : 0;
+    const size_t lds = k_lds + v_lds + o_lds;
     if (a.causal || a.kpad) return dispatch_16bit_mode<T, D, true>(nkc, grid, lds, st, a);
     return dispatch_16bit_mode<T, D, false>(nkc, grid, lds, st, a);
 }

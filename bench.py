@@ -54,6 +54,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--batch", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--qkv", choices=("separate", "packed"), default="separate",
+                    help="q/k/v as three tensors or as views of one fused [B, L, 3E] projection")
     ap.add_argument("--no-extras", action="store_true", help="skip the e2e and kq_policy legs")
     ap.add_argument("--cpu-sample", type=int, default=1024, help="batch of the CPU baseline sample")
     ap.add_argument(
@@ -83,8 +85,10 @@ def pmc_workload(torch, ops, batch, steps, dev) -> None:
     print(f"[pmc] attention x{steps} (B={batch}) and 1 GiB copy x{steps} done", file=sys.stderr, flush=True)
 
 
-def make_layers(torch, batch, seq, embed, layers, dev):
-    """Per-layer resident (q, k, v) of shape [B, L, H, D] (views of [B, L, E])."""
+def make_layers(torch, batch, seq, embed, layers, dev, packed=False):
+    """Per-layer resident (q, k, v), each [B, L, E].  ``packed``: one fused
+    QKV projection per layer, q/k/v being strided views of its [B, L, 3E]
+    output; otherwise three separate projections (three tensors)."""
     g = torch.Generator(device=dev).manual_seed(45)
     x = torch.randn(batch, seq, embed, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
     out = []
@@ -93,7 +97,11 @@ def make_layers(torch, batch, seq, embed, layers, dev):
             (torch.randn(embed, embed, generator=g, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
             for _ in range(3)
         ]
-        out.append(tuple(torch.matmul(x, wi) for wi in w))
+        if packed:
+            qkv = torch.matmul(x, torch.cat(w, dim=1))
+            out.append((qkv[..., :embed], qkv[..., embed : 2 * embed], qkv[..., 2 * embed :]))
+        else:
+            out.append(tuple(torch.matmul(x, wi) for wi in w))
     del x
     return out
 
@@ -101,7 +109,7 @@ def make_layers(torch, batch, seq, embed, layers, dev):
 def time_attention(torch, ops, layers, heads, head_dim, steps, warmup):
     """Time `steps` passes over all layers; return (ms_per_step, mean kernel ms)."""
     b, l, e = layers[0][0].shape
-    views = [tuple(t.view(b, l, heads, head_dim) for t in qkv) for qkv in layers]
+    views = [tuple(t.unflatten(-1, (heads, head_dim)) for t in qkv) for qkv in layers]
     outs = [torch.empty(b, l, heads, head_dim, dtype=torch.bfloat16, device=layers[0][0].device) for _ in layers]
     for _ in range(warmup):
         for (q, k, v), o in zip(views, outs):
@@ -228,7 +236,7 @@ def main() -> int:
         return 0
     batch, seq, embed, heads, head_dim = args.batch, 100, 384, 6, 64
     t0 = time.time()
-    layers = make_layers(torch, batch, seq, embed, args.layers, dev)
+    layers = make_layers(torch, batch, seq, embed, args.layers, dev, packed=args.qkv == "packed")
     torch.cuda.synchronize()
     print(f"[bench] inputs ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
 
