@@ -75,26 +75,46 @@ __device__ inline uint64_t key_valid_bits(const AttnArgs& a, int b, int g, int n
 // is not monotonic in this target (a looser budget can make it hoist loads
 // far enough to spill), so the values were found by compiling every
 // instantiation at every target, not by a formula.
-constexpr int kOcc16[2][8][8] = {
+constexpr int kOcc16[4][8][8] = {
     {
-        {8, 8, 8, 7, 6, 5, 5, 4},
-        {8, 8, 8, 7, 6, 5, 5, 4},
-        {8, 8, 7, 6, 5, 5, 4, 4},
-        {6, 6, 5, 5, 5, 4, 4, 4},
-        {7, 6, 6, 5, 5, 4, 4, 4},
-        {6, 6, 5, 5, 4, 4, 3, 3},
-        {5, 5, 5, 4, 4, 3, 3, 3},
-        {4, 4, 4, 4, 4, 3, 3, 3},
+        {8, 8, 8, 8, 8, 7, 6, 5},
+        {8, 8, 8, 8, 8, 7, 5, 5},
+        {8, 8, 8, 8, 7, 6, 5, 5},
+        {7, 8, 7, 7, 6, 5, 5, 4},
+        {8, 8, 7, 5, 6, 5, 5, 4},
+        {7, 7, 6, 6, 5, 5, 4, 4},
+        {6, 5, 5, 5, 5, 4, 4, 4},
+        {4, 4, 3, 4, 4, 4, 4, 4},
     },
     {
-        {8, 8, 6, 5, 4, 3, 3, 2},
-        {8, 8, 8, 5, 4, 3, 3, 2},
-        {8, 8, 5, 5, 4, 3, 3, 3},
-        {8, 7, 6, 4, 4, 3, 3, 2},
-        {8, 7, 6, 6, 4, 4, 3, 3},
-        {7, 6, 5, 5, 4, 4, 3, 3},
-        {6, 5, 4, 5, 4, 3, 3, 3},
-        {5, 4, 4, 4, 4, 3, 3, 2},
+        {8, 8, 8, 8, 8, 7, 6, 5},
+        {8, 8, 8, 8, 7, 6, 5, 5},
+        {8, 8, 8, 7, 6, 5, 5, 4},
+        {7, 8, 7, 7, 6, 5, 5, 4},
+        {8, 7, 7, 6, 5, 5, 4, 4},
+        {7, 6, 6, 6, 5, 5, 4, 4},
+        {6, 6, 5, 5, 4, 4, 4, 4},
+        {4, 4, 4, 4, 4, 4, 4, 3},
+    },
+    {
+        {8, 8, 8, 8, 7, 6, 5, 4},
+        {8, 8, 8, 8, 7, 6, 5, 4},
+        {8, 8, 8, 7, 6, 5, 4, 4},
+        {7, 8, 7, 6, 5, 5, 4, 4},
+        {8, 7, 7, 6, 5, 5, 4, 4},
+        {7, 7, 6, 6, 5, 4, 3, 4},
+        {6, 6, 5, 5, 5, 4, 4, 4},
+        {4, 4, 4, 4, 4, 4, 4, 3},
+    },
+    {
+        {8, 8, 8, 8, 6, 5, 5, 4},
+        {8, 8, 8, 8, 6, 5, 5, 4},
+        {8, 8, 8, 7, 5, 5, 4, 4},
+        {8, 7, 7, 6, 5, 4, 4, 4},
+        {8, 8, 7, 6, 5, 4, 4, 4},
+        {7, 7, 6, 5, 4, 4, 4, 4},
+        {6, 6, 5, 5, 4, 4, 4, 3},
+        {4, 4, 4, 4, 4, 4, 3, 3},
     },
 };
 constexpr int kOcc32[8][8] = {
@@ -107,9 +127,9 @@ constexpr int kOcc32[8][8] = {
     {7, 5, 4, 4, 3, 3, 3, 2},
     {7, 5, 4, 4, 3, 3, 2, 2},
 };
-template <int D, int NKC, bool MASKED>
+template <int D, int NKC, bool MASKED, bool FULL>
 constexpr int occ_16bit() {
-    return kOcc16[MASKED ? 1 : 0][D / 16 - 1][NKC - 1];
+    return kOcc16[(MASKED ? 2 : 0) + (FULL ? 1 : 0)][D / 16 - 1][NKC - 1];
 }
 template <int D, int NKC>
 constexpr int occ_fp32() {
@@ -130,29 +150,31 @@ constexpr bool kStagedStores = (D == 64 || D == 128);
 
 // ---------------------------------------------------------------------------
 // 16-bit inputs (bf16 / fp16).  NKC = number of 32-key chunks (S_kv <= 32*NKC);
-// MASKED selects the variant with causal / key-padding masks, so the plain
-// kernel carries no per-element mask work beyond the key bound of its last
-// tile.
+// FULL = the last 16-key tile of the last chunk exists (S_kv > 32*NKC - 16),
+// so the number of key tiles is a compile-time constant; MASKED selects the
+// variant with causal / key-padding masks, so the plain kernel carries no
+// per-element mask work beyond the key bound of its last tile.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int NKC, bool MASKED>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(occ_16bit<D, NKC, MASKED>(), 8)))
+template <typename T, int D, int NKC, bool MASKED, bool FULL>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(occ_16bit<D, NKC, MASKED, FULL>(), 8)))
 void attn_fwd_16bit(AttnArgs a) {
     using M = Mfma16<T>;
     constexpr int CH = D / 8;          // 16-byte chunks per row
     constexpr int NI = (D + 31) / 32;  // QK^T MFMAs per 16x16 tile
     constexpr int NDT = D / 16;        // PV output tiles
     constexpr int QD = D / 4;          // contiguous outputs per lane
-    constexpr int NKT = 2 * NKC;
+    constexpr int NKT = FULL ? 2 * NKC : 2 * NKC - 1;  // key tiles
+    constexpr int ROWS = NKT * 16;     // K / V rows staged
     constexpr bool KSWZ = kKeySwizzle<D>;   // K rows XOR-swizzled instead of padded
     constexpr int RSK = K_row_bytes<D>();   // K row stride in LDS (bytes)
     constexpr int RSV = D * 2;              // V row stride in LDS (bytes, 8-byte units swizzled)
     constexpr bool STAGE_OUT = kStagedStores<D>;  // whole-line output stores through LDS
     constexpr int OROWS = 8;                // output rows staged per round
+    constexpr int KIT = (ROWS * CH + kThreads - 1) / kThreads;
 
-    const int nkt = a.nkt;  // 2*NKC or 2*NKC - 1
     lds_t* const sk = lds_base();
-    lds_t* const sv = sk + nkt * 16 * RSK;
-    lds_t* const so = sv + nkt * 16 * RSV;  // per-wave output staging (STAGE_OUT)
+    lds_t* const sv = sk + ROWS * RSK;
+    lds_t* const so = sv + ROWS * RSV;  // per-wave output staging (STAGE_OUT)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -169,57 +191,44 @@ void attn_fwd_16bit(AttnArgs a) {
 
     const int nqt = (a.Sq + 15) >> 4;
 
-    // Q operand (B of S^T = K Q^T): lane (m, g) holds chunk 4i+g of query row m.
+    // Q operand (B of S^T = K Q^T): lane (m, g) holds chunk 4i+g of query row
+    // m.  Rows past S_q re-read row S_q - 1; their results are never stored.
     auto load_q = [&](int qt, u32x4 (&qop)[NI]) {
-        const int qrow = qt * 16 + m;
+        const int qrow = min(qt * 16 + m, a.Sq - 1);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int c = 4 * i + g;
-            qop[i] = (qrow < a.Sq && c < CH) ? ld16_stream(qb + qrow * qss + c * 8) : u32x4{0, 0, 0, 0};
+            qop[i] = (CH % 4 == 0 || c < CH) ? ld16_stream(qb + qrow * qss + c * 8) : u32x4{0, 0, 0, 0};
         }
     };
     u32x4 qop[NI];
     if (wave < nqt) load_q(wave, qop);
 
-    // ---- stage K (row-major; rows from S_kv up to the last tile are zero).
-    //      With 8 or 16 chunks per row the 16-byte chunk c of row r sits at
-    //      c ^ ((r >> 1) & 7); otherwise rows are padded to an odd number of
-    //      16-byte units.  Either way the 16 rows of one MFMA operand read
-    //      fall in distinct bank groups. --------------------------------------
-    constexpr int KIT = (NKT * 16 * CH + kThreads - 1) / kThreads;
-    u32x4 kreg[KIT];
-    const int kchunks = nkt * 16 * CH;
+    // ---- stage K and V rows 0 .. ROWS-1.  Row indices are clamped to
+    //      S_kv - 1, so padding rows hold finite copies: padded keys are
+    //      masked by the -inf bias and padded values meet P = 0. -------------
+    u32x4 kreg[KIT], vreg[KIT];
 #pragma unroll
     for (int it = 0; it < KIT; ++it) {
         const int idx = tid + it * kThreads;
         const int r = idx / CH, c = idx - r * CH;
-        kreg[it] = (idx < kchunks && r < a.Skv) ? ld16_stream(kb + r * kss + c * 8) : u32x4{0, 0, 0, 0};
+        const int rr = min(r, a.Skv - 1);
+        kreg[it] = ld16_stream(kb + rr * kss + c * 8);
+        vreg[it] = ld16_stream(vb + rr * vss + c * 8);
     }
-    // ---- stage V (row-major, rows up to the last tile; rows past S_kv zero)
-    constexpr int VIT = KIT;
-    u32x4 vreg[VIT];
-#pragma unroll
-    for (int it = 0; it < VIT; ++it) {
-        const int idx = tid + it * kThreads;
-        const int r = idx / CH, c = idx - r * CH;
-        vreg[it] = (idx < kchunks && r < a.Skv) ? ld16_stream(vb + r * vss + c * 8) : u32x4{0, 0, 0, 0};
-    }
+    // K: with 8 or 16 chunks per row the 16-byte chunk c of row r sits at
+    // c ^ ((r >> 1) & 7); otherwise rows are padded to an odd number of 16-byte
+    // units.  Either way the 16 rows of one MFMA operand read fall in distinct
+    // bank groups.  V: the 8-byte units of row r sit at unit ^ s(r),
+    // s(r) = ((r >> 1) ^ r) & 3, so the transposing reads below touch distinct
+    // bank pairs.
 #pragma unroll
     for (int it = 0; it < KIT; ++it) {
         const int idx = tid + it * kThreads;
-        if (idx < kchunks) {
+        if ((ROWS * CH) % kThreads == 0 || idx < ROWS * CH) {
             const int r = idx / CH, c = idx - r * CH;
             const int pc = KSWZ ? (c ^ ((r >> 1) & 7)) : c;
             lds_st16(sk + r * RSK + pc * 16, kreg[it]);
-        }
-    }
-    // The 8-byte units of V row r sit at unit ^ s(r), s(r) = ((r >> 1) ^ r) & 3:
-    // the transposing reads below then touch 32 distinct bank pairs per phase.
-#pragma unroll
-    for (int it = 0; it < VIT; ++it) {
-        const int idx = tid + it * kThreads;
-        if (idx < kchunks) {
-            const int r = idx / CH, c = idx - r * CH;
             const int sw = ((r >> 1) ^ r) & 3;
             lds_t* row = sv + r * RSV;
             lds_st8(row + (((2 * c) ^ sw) << 3), u32x2{vreg[it][0], vreg[it][1]});
@@ -227,67 +236,72 @@ void attn_fwd_16bit(AttnArgs a) {
         }
     }
 
+    uint64_t kbits = 0;
+    if constexpr (MASKED) kbits = key_valid_bits(a, b, g, NKT);
     const float c2 = a.c2;
     const float kNegInf = -__builtin_inff();
-    uint64_t kbits = 0;
-    if constexpr (MASKED) kbits = key_valid_bits(a, b, g, nkt);
-    const bool last_full = (nkt == NKT);
-    // Keys at or past S_kv can only sit in the last two tiles (S_kv > 16*(NKT-2)):
+    // Keys at or past S_kv can only sit in the last tile (S_kv > 16*(NKT-1)):
     // an additive 0 / -inf bias per lane masks them with one add per score.
-    float kbias[2][4];
+    float kbias[4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kbias[j][i] = ((NKT - 2 + j) * 16 + 4 * g + i < a.Skv) ? 0.f : kNegInf;
-    __syncthreads();
+    for (int i = 0; i < 4; ++i) kbias[i] = ((NKT - 1) * 16 + 4 * g + i < a.Skv) ? 0.f : kNegInf;
 
-    // Transposing-read geometry of this lane (ds_read_b64_tr_b16): input lane
-    // i = a4 + 4t of a 16-lane group points at row 4g + t (+32c + 16h) and
-    // columns a4*QD + 4dt..+3; the read hands lane m the four keys of its
-    // group for head-dim (m/4)*QD + 4dt + m%4.
-    const int tr_t = m >> 2, tr_a = m & 3;
-    const int tr_row = 4 * g + tr_t;
+    // Per-lane LDS addresses, fixed for the whole workgroup; tile, chunk and
+    // half offsets are compile-time and fold into the instructions' offsets.
+    //  K operand: row m of each 16-key tile, chunk 4i+g (swizzled).
+    //  V^T operand (ds_read_b64_tr_b16): input lane i = a4 + 4t of a 16-lane
+    //  group points at row 4g + t (+32c + 16h) and columns a4*QD + 4dt..+3;
+    //  the read hands lane m the four keys of its group for head-dim
+    //  (m/4)*QD + 4dt + m%4.
+    lds_t* k_lane[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int c = 4 * i + g;
+        k_lane[i] = sk + m * RSK + (KSWZ ? (c ^ ((m >> 1) & 7)) : c) * 16;
+    }
+    const int tr_row = 4 * g + (m >> 2);
     const int tr_sw = ((tr_row >> 1) ^ tr_row) & 3;
+    lds_t* v_lane[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) v_lane[dt] = sv + tr_row * RSV + ((((m & 3) * NDT + dt) ^ tr_sw) << 3);
+    lds_t* const o_wave = so + wave * (OROWS * 2 * D);
+    lds_t* o_put = o_wave + (m & 7) * (2 * D) + g * (QD * 2);
     const uint32_t ones = M::kOnes2;
+    __syncthreads();
 
     for (int qt = wave; qt < nqt; qt += kWaves) {
         const int qrow = qt * 16 + m;
-        lds_t* const skq = lds_opaque(sk);
-        lds_t* const svq = lds_opaque(sv);
+        // The asm barrier below makes every LDS address look new on each
+        // pass, so the compiler cannot hoist the (loop-invariant) operand reads
+        // of all tiles out of the loop, which would need far more registers.
+        lds_t* kl[NI];
+        lds_t* vl[NDT];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) kl[i] = lds_opaque(k_lane[i]);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) vl[dt] = lds_opaque(v_lane[dt]);
 
         // ---- S^T = K Q^T over the key tiles -------------------------------
         f32x4 s[NKT];
-        auto tile_scores = [&](int kt) {
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
             f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-            const lds_t* krow = skq + (kt * 16 + m) * RSK;
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
-                const int c = 4 * i + g;
-                // (kt*16 + m) >> 1 has the same low three bits as m >> 1.
-                const int pc = KSWZ ? (c ^ ((m >> 1) & 7)) : c;
-                u32x4 kop = lds_ld16(krow + pc * 16);
-                if (CH % 4 != 0 && c >= CH) kop = u32x4{0, 0, 0, 0};
+                u32x4 kop = lds_ld16(kl[i] + kt * 16 * RSK);
+                if (CH % 4 != 0 && 4 * i + g >= CH) kop = u32x4{0, 0, 0, 0};
                 acc = M::mma(kop, qop[i], acc);
             }
-            return acc;
-        };
-#pragma unroll
-        for (int kt = 0; kt < NKT - 1; ++kt) s[kt] = tile_scores(kt);
-        // The last tile exists only when S_kv > 16*(NKT-1); otherwise its
-        // scores are -inf and its probabilities come out as exp2(-inf) = 0.
-        if (last_full) {
-            s[NKT - 1] = tile_scores(NKT - 1);
-        } else {
-            s[NKT - 1] = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
+            s[kt] = acc;
         }
         if (qt + kWaves < nqt) load_q(qt + kWaves, qop);
         // Phase fence: keeps the PV operand reads below the softmax.
         __builtin_amdgcn_sched_barrier(0);
 
         // ---- mask -----------------------------------------------------------
+        if constexpr (MASKED) {
 #pragma unroll
-        for (int kt = 0; kt < NKT; ++kt) {
-            if constexpr (MASKED) {
+            for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int key = kt * 16 + 4 * g + i;
@@ -295,10 +309,9 @@ void attn_fwd_16bit(AttnArgs a) {
                     if (a.causal) ok = ok && key <= qrow;
                     s[kt][i] = ok ? s[kt][i] : kNegInf;
                 }
-            } else if (kt >= NKT - 2) {
+        } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) s[kt][i] += kbias[kt - (NKT - 2)][i];
-            }
+            for (int i = 0; i < 4; ++i) s[NKT - 1][i] += kbias[i];
         }
 
         // ---- single-pass softmax over the whole key row ---------------------
@@ -316,11 +329,10 @@ void attn_fwd_16bit(AttnArgs a) {
         for (int c = 0; c < NKC; ++c) {
             float p[8];
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int kt = 2 * c + hh;
+            for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) p[4 * hh + i] = fast_exp2(__builtin_fmaf(s[kt][i], c2, -mb));
-            }
+                for (int i = 0; i < 4; ++i)
+                    p[4 * hh + i] = (2 * c + hh < NKT) ? fast_exp2(__builtin_fmaf(s[(2 * c + hh) % NKT][i], c2, -mb)) : 0.f;
             pk[c] = u32x4{M::pack2(p[0], p[1]), M::pack2(p[2], p[3]), M::pack2(p[4], p[5]), M::pack2(p[6], p[7])};
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -333,13 +345,11 @@ void attn_fwd_16bit(AttnArgs a) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
             oacc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-            const lds_t* vlane = svq + tr_row * RSV + ((((tr_a * NDT) + dt) ^ tr_sw) << 3);
 #pragma unroll
             for (int c = 0; c < NKC; ++c) {
-                const u32x2 lo = lds_ld8_tr16(vlane + (32 * c) * RSV);
-                // V rows exist up to the last tile; a missing tile has P = 0.
-                u32x2 hi = u32x2{0u, 0u};
-                if (c < NKC - 1 || last_full) hi = lds_ld8_tr16(vlane + (32 * c + 16) * RSV);
+                const u32x2 lo = lds_ld8_tr16(vl[dt] + (32 * c) * RSV);
+                // A missing last tile has P = 0 and no V rows.
+                const u32x2 hi = (2 * c + 1 < NKT) ? lds_ld8_tr16(vl[dt] + (32 * c + 16) * RSV) : u32x2{0u, 0u};
                 oacc[dt] = M::mma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[c], oacc[dt]);
             }
         }
@@ -349,18 +359,18 @@ void attn_fwd_16bit(AttnArgs a) {
         //      writes whole 128-byte rows with the streaming hint ------------
         const float inv = fast_rcp(lsum4[0]);
         if constexpr (STAGE_OUT) {
-            lds_t* const sow = lds_opaque(so) + wave * (OROWS * 2 * D);
+            lds_t* const put = lds_opaque(o_put);
+            lds_t* const tile = lds_opaque(o_wave);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 if ((m >> 3) == j) {
-                    lds_t* dst = sow + (m & 7) * (2 * D) + g * (QD * 2);
 #pragma unroll
                     for (int dt = 0; dt < NDT; dt += 2) {
                         const u32x4 w = {M::pack2(oacc[dt][0] * inv, oacc[dt][1] * inv),
                                          M::pack2(oacc[dt][2] * inv, oacc[dt][3] * inv),
                                          M::pack2(oacc[dt + 1][0] * inv, oacc[dt + 1][1] * inv),
                                          M::pack2(oacc[dt + 1][2] * inv, oacc[dt + 1][3] * inv)};
-                        lds_st16(dst + dt * 8, w);
+                        lds_st16(put + dt * 8, w);
                     }
                 }
                 // LDS accesses of one wave complete in order: the reads see
@@ -369,7 +379,7 @@ void attn_fwd_16bit(AttnArgs a) {
                 for (int k = 0; k < CH / 8; ++k) {
                     const int idx = lane + 64 * k;
                     const int row = idx / CH, c = idx - row * CH;
-                    const u32x4 w = lds_ld16(sow + row * (2 * D) + c * 16);
+                    const u32x4 w = lds_ld16(tile + row * (2 * D) + c * 16);
                     const int orow_i = qt * 16 + OROWS * j + row;
                     if (orow_i < a.Sq) st16_stream(ob + orow_i * oss + c * 8, w);
                 }
@@ -562,17 +572,17 @@ int launch(Kernel kernel, int grid, size_t lds, hipStream_t stream, const AttnAr
     return ATX_OK;
 }
 
-template <typename T, int D, bool MASKED>
+template <typename T, int D, bool MASKED, bool FULL>
 int dispatch_16bit_mode(int nkc, int grid, size_t lds, hipStream_t st, const AttnArgs& a) {
     switch (nkc) {
-        case 1: return launch(attn_fwd_16bit<T, D, 1, MASKED>, grid, lds, st, a);
-        case 2: return launch(attn_fwd_16bit<T, D, 2, MASKED>, grid, lds, st, a);
-        case 3: return launch(attn_fwd_16bit<T, D, 3, MASKED>, grid, lds, st, a);
-        case 4: return launch(attn_fwd_16bit<T, D, 4, MASKED>, grid, lds, st, a);
-        case 5: return launch(attn_fwd_16bit<T, D, 5, MASKED>, grid, lds, st, a);
-        case 6: return launch(attn_fwd_16bit<T, D, 6, MASKED>, grid, lds, st, a);
-        case 7: return launch(attn_fwd_16bit<T, D, 7, MASKED>, grid, lds, st, a);
-        case 8: return launch(attn_fwd_16bit<T, D, 8, MASKED>, grid, lds, st, a);
+        case 1: return launch(attn_fwd_16bit<T, D, 1, MASKED, FULL>, grid, lds, st, a);
+        case 2: return launch(attn_fwd_16bit<T, D, 2, MASKED, FULL>, grid, lds, st, a);
+        case 3: return launch(attn_fwd_16bit<T, D, 3, MASKED, FULL>, grid, lds, st, a);
+        case 4: return launch(attn_fwd_16bit<T, D, 4, MASKED, FULL>, grid, lds, st, a);
+        case 5: return launch(attn_fwd_16bit<T, D, 5, MASKED, FULL>, grid, lds, st, a);
+        case 6: return launch(attn_fwd_16bit<T, D, 6, MASKED, FULL>, grid, lds, st, a);
+        case 7: return launch(attn_fwd_16bit<T, D, 7, MASKED, FULL>, grid, lds, st, a);
+        case 8: return launch(attn_fwd_16bit<T, D, 8, MASKED, FULL>, grid, lds, st, a);
     }
     ATX_FAIL(ATX_ERR_UNSUPPORTED, "seq_kv chunk count %d", nkc);
 }
@@ -583,8 +593,14 @@ int dispatch_16bit(int nkc, int grid, hipStream_t st, const AttnArgs& a) {
     const size_t v_lds = (size_t)a.nkt * 16 * D * 2;
     const size_t o_lds = kStagedStores<D> ? (size_t)kWaves * 8 * D * 2 : 0;
     const size_t lds = k_lds + v_lds + o_lds;
-    if (a.causal || a.kpad) return dispatch_16bit_mode<T, D, true>(nkc, grid, lds, st, a);
-    return dispatch_16bit_mode<T, D, false>(nkc, grid, lds, st, a);
+    const bool masked = a.causal || a.kpad;
+    const bool full = a.nkt == 2 * nkc;
+    if (masked) {
+        return full ? dispatch_16bit_mode<T, D, true, true>(nkc, grid, lds, st, a)
+                    : dispatch_16bit_mode<T, D, true, false>(nkc, grid, lds, st, a);
+    }
+    return full ? dispatch_16bit_mode<T, D, false, true>(nkc, grid, lds, st, a)
+                : dispatch_16bit_mode<T, D, false, false>(nkc, grid, lds, st, a);
 }
 
 template <int D>

@@ -154,13 +154,15 @@ __device__ inline void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v
 __device__ inline void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
 
 // Streaming variants (nontemporal hint) for data touched exactly once.  On
-// MI355X the hint is neutral for the attention kernel's loads and costs about
-// 4 % on its stores (C3, measured side by side), so stores default to plain.
+// MI355X a streaming store pays off only when each store instruction writes
+// whole 128-byte lines (measured: whole lines 214 us vs 229 us plain for the
+// attention traffic of C3; half lines per instruction 235 us), which is how
+// the attention kernel stages its output rows.
 #ifndef ATX_STREAM_LOADS
 #define ATX_STREAM_LOADS 1
 #endif
 #ifndef ATX_STREAM_STORES
-#define ATX_STREAM_STORES 0
+#define ATX_STREAM_STORES 1
 #endif
 __device__ inline u32x4 ld16_stream(const void* p) {
     if constexpr (ATX_STREAM_LOADS) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
