@@ -78,43 +78,43 @@ __device__ inline uint64_t key_valid_bits(const AttnArgs& a, int b, int g, int n
 constexpr int kOcc16[4][8][8] = {
     {
         {8, 8, 8, 8, 8, 7, 6, 5},
-        {8, 8, 8, 8, 8, 7, 5, 5},
+        {8, 8, 8, 8, 8, 7, 6, 5},
         {8, 8, 8, 8, 7, 6, 5, 5},
-        {7, 8, 7, 7, 6, 5, 5, 4},
-        {8, 8, 7, 5, 6, 5, 5, 4},
-        {7, 7, 6, 6, 5, 5, 4, 4},
-        {6, 5, 5, 5, 5, 4, 4, 4},
-        {4, 4, 3, 4, 4, 4, 4, 4},
+        {8, 8, 7, 7, 6, 5, 5, 4},
+        {8, 7, 7, 6, 6, 5, 5, 4},
+        {7, 7, 6, 6, 5, 5, 5, 4},
+        {6, 5, 5, 5, 5, 5, 4, 4},
+        {5, 5, 4, 4, 4, 4, 4, 4},
     },
     {
         {8, 8, 8, 8, 8, 7, 6, 5},
+        {8, 8, 8, 8, 8, 7, 6, 5},
         {8, 8, 8, 8, 7, 6, 5, 5},
         {8, 8, 8, 7, 6, 5, 5, 4},
-        {7, 8, 7, 7, 6, 5, 5, 4},
-        {8, 7, 7, 6, 5, 5, 4, 4},
-        {7, 6, 6, 6, 5, 5, 4, 4},
-        {6, 6, 5, 5, 4, 4, 4, 4},
-        {4, 4, 4, 4, 4, 4, 4, 3},
+        {8, 7, 6, 6, 5, 5, 4, 4},
+        {8, 6, 6, 6, 5, 5, 4, 4},
+        {7, 5, 5, 5, 4, 4, 4, 4},
+        {5, 5, 4, 4, 4, 4, 4, 4},
     },
     {
         {8, 8, 8, 8, 7, 6, 5, 4},
         {8, 8, 8, 8, 7, 6, 5, 4},
-        {8, 8, 8, 7, 6, 5, 4, 4},
-        {7, 8, 7, 6, 5, 5, 4, 4},
-        {8, 7, 7, 6, 5, 5, 4, 4},
-        {7, 7, 6, 6, 5, 4, 3, 4},
+        {8, 8, 8, 8, 6, 5, 5, 4},
+        {8, 7, 5, 4, 4, 3, 3, 2},
+        {8, 8, 7, 6, 5, 5, 4, 4},
+        {7, 7, 6, 6, 5, 4, 4, 4},
         {6, 6, 5, 5, 5, 4, 4, 4},
-        {4, 4, 4, 4, 4, 4, 4, 3},
+        {4, 4, 4, 4, 3, 3, 2, 2},
     },
     {
+        {8, 8, 8, 8, 7, 5, 5, 4},
         {8, 8, 8, 8, 6, 5, 5, 4},
-        {8, 8, 8, 8, 6, 5, 5, 4},
-        {8, 8, 8, 7, 5, 5, 4, 4},
-        {8, 7, 7, 6, 5, 4, 4, 4},
-        {8, 8, 7, 6, 5, 4, 4, 4},
-        {7, 7, 6, 5, 4, 4, 4, 4},
-        {6, 6, 5, 5, 4, 4, 4, 3},
-        {4, 4, 4, 4, 4, 4, 3, 3},
+        {8, 8, 8, 7, 6, 5, 4, 4},
+        {7, 6, 5, 4, 4, 3, 3, 2},
+        {8, 7, 6, 6, 5, 4, 4, 4},
+        {8, 7, 6, 6, 5, 4, 4, 4},
+        {7, 6, 5, 5, 5, 4, 4, 4},
+        {4, 3, 4, 3, 3, 3, 2, 2},
     },
 };
 constexpr int kOcc32[8][8] = {
@@ -184,37 +184,38 @@ void attn_fwd_16bit(AttnArgs a) {
     const int hk = h / a.group;
     const int qss = (int)a.qss, kss = (int)a.kss, vss = (int)a.vss, oss = (int)a.oss;
 
-    const T* kb = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
-    const T* vb = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
-    const T* qb = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
+    // One buffer descriptor per tensor slice of this (batch, head); each ends
+    // at the last valid row, so rows past S_q / S_kv read as zero and output
+    // rows past S_q are not written.
+    const rsrc_t rk = make_rsrc(static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh, ((a.Skv - 1) * kss + D) * 2);
+    const rsrc_t rv = make_rsrc(static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh, ((a.Skv - 1) * vss + D) * 2);
+    const rsrc_t rq = make_rsrc(static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh, ((a.Sq - 1) * qss + D) * 2);
+    const rsrc_t ro = make_rsrc(static_cast<T*>(a.o) + b * a.osb + h * a.osh, ((a.Sq - 1) * oss + D) * 2);
     T* ob = static_cast<T*>(a.o) + b * a.osb + h * a.osh;
 
     const int nqt = (a.Sq + 15) >> 4;
 
-    // Q operand (B of S^T = K Q^T): lane (m, g) holds chunk 4i+g of query row
-    // m.  Rows past S_q re-read row S_q - 1; their results are never stored.
+    // Q operand (B of S^T = K Q^T): lane (m, g) holds chunk 4i+g of query row m.
     auto load_q = [&](int qt, u32x4 (&qop)[NI]) {
-        const int qrow = min(qt * 16 + m, a.Sq - 1);
+        const uint32_t qrow = qt * 16 + m;
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int c = 4 * i + g;
-            qop[i] = (CH % 4 == 0 || c < CH) ? ld16_stream(qb + qrow * qss + c * 8) : u32x4{0, 0, 0, 0};
+            qop[i] = (CH % 4 == 0 || c < CH) ? buf_ld16(rq, (qrow * qss + c * 8) * 2) : u32x4{0, 0, 0, 0};
         }
     };
     u32x4 qop[NI];
     if (wave < nqt) load_q(wave, qop);
 
-    // ---- stage K and V rows 0 .. ROWS-1.  Row indices are clamped to
-    //      S_kv - 1, so padding rows hold finite copies: padded keys are
-    //      masked by the -inf bias and padded values meet P = 0. -------------
+    // ---- stage K and V rows 0 .. ROWS-1 (rows past S_kv read as zero:
+    //      padded keys are masked by the -inf bias, padded values meet P = 0)
     u32x4 kreg[KIT], vreg[KIT];
 #pragma unroll
     for (int it = 0; it < KIT; ++it) {
         const int idx = tid + it * kThreads;
-        const int r = idx / CH, c = idx - r * CH;
-        const int rr = min(r, a.Skv - 1);
-        kreg[it] = ld16_stream(kb + rr * kss + c * 8);
-        vreg[it] = ld16_stream(vb + rr * vss + c * 8);
+        const uint32_t r = idx / CH, c = idx - r * CH;
+        kreg[it] = buf_ld16(rk, (r * kss + c * 8) * 2);
+        vreg[it] = buf_ld16(rv, (r * vss + c * 8) * 2);
     }
     // K: with 8 or 16 chunks per row the 16-byte chunk c of row r sits at
     // c ^ ((r >> 1) & 7); otherwise rows are padded to an odd number of 16-byte
@@ -361,28 +362,28 @@ void attn_fwd_16bit(AttnArgs a) {
         if constexpr (STAGE_OUT) {
             lds_t* const put = lds_opaque(o_put);
             lds_t* const tile = lds_opaque(o_wave);
+            u32x4 w[NDT / 2];
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt += 2)
+                w[dt / 2] = u32x4{M::pack2(oacc[dt][0] * inv, oacc[dt][1] * inv),
+                                  M::pack2(oacc[dt][2] * inv, oacc[dt][3] * inv),
+                                  M::pack2(oacc[dt + 1][0] * inv, oacc[dt + 1][1] * inv),
+                                  M::pack2(oacc[dt + 1][2] * inv, oacc[dt + 1][3] * inv)};
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 if ((m >> 3) == j) {
 #pragma unroll
-                    for (int dt = 0; dt < NDT; dt += 2) {
-                        const u32x4 w = {M::pack2(oacc[dt][0] * inv, oacc[dt][1] * inv),
-                                         M::pack2(oacc[dt][2] * inv, oacc[dt][3] * inv),
-                                         M::pack2(oacc[dt + 1][0] * inv, oacc[dt + 1][1] * inv),
-                                         M::pack2(oacc[dt + 1][2] * inv, oacc[dt + 1][3] * inv)};
-                        lds_st16(put + dt * 8, w);
-                    }
+                    for (int dt = 0; dt < NDT; dt += 2) lds_st16(put + dt * 8, w[dt / 2]);
                 }
-                // LDS accesses of one wave complete in order: the reads see
-                // the writes above, and the next round's writes follow them.
+                wave_lds_handoff();  // the reads below see the writes above
 #pragma unroll
                 for (int k = 0; k < CH / 8; ++k) {
                     const int idx = lane + 64 * k;
-                    const int row = idx / CH, c = idx - row * CH;
-                    const u32x4 w = lds_ld16(tile + row * (2 * D) + c * 16);
-                    const int orow_i = qt * 16 + OROWS * j + row;
-                    if (orow_i < a.Sq) st16_stream(ob + orow_i * oss + c * 8, w);
+                    const uint32_t row = idx / CH, c = idx - row * CH;
+                    const u32x4 v = lds_ld16(tile + row * (2 * D) + c * 16);
+                    buf_st16(ro, ((qt * 16 + OROWS * j + row) * oss + c * 8) * 2, v);
                 }
+                wave_lds_handoff();  // the next round's writes follow these reads
             }
         } else if (qrow < a.Sq) {
             T* orow = ob + qrow * oss + g * QD;
@@ -682,21 +683,40 @@ extern "C" int atx_attn_fwd(const AtxAttnParams* p, void* stream) {
     const int64_t grid = (int64_t)p->batch * p->num_heads;
     if (grid > 0x7fffffff) ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_fwd: batch*heads %lld too large", (long long)grid);
     const int es = p->dtype == ATX_DTYPE_FP32 ? 4 : 2;
-    if (!rows_aligned(p->q, p->q_stride_b, p->q_stride_s, p->q_stride_h, es) ||
-        !rows_aligned(p->k, p->k_stride_b, p->k_stride_s, p->k_stride_h, es) ||
-        !rows_aligned(p->v, p->v_stride_b, p->v_stride_s, p->v_stride_h, es) ||
-        !rows_aligned(p->o, p->o_stride_b, p->o_stride_s, p->o_stride_h, es))
+    // The 16-bit kernels address one (batch, head) slice through a buffer
+    // descriptor that ends at the last valid row: rows past the sequence read
+    // as zero and output rows past it are dropped. That needs 32-bit byte
+    // offsets (rows up to the next multiple of 16 past the end) and output
+    // rows that do not overlap. A length-1 sequence's stride is never used
+    // to reach a valid row, so it is replaced by one row's extent.
+    const int64_t qss = p->seq_q == 1 ? p->head_dim : p->q_stride_s;
+    const int64_t oss = p->seq_q == 1 ? p->head_dim : p->o_stride_s;
+    const int64_t kss = p->seq_kv == 1 ? p->head_dim : p->k_stride_s;
+    const int64_t vss = p->seq_kv == 1 ? p->head_dim : p->v_stride_s;
+    if (!rows_aligned(p->q, p->q_stride_b, qss, p->q_stride_h, es) ||
+        !rows_aligned(p->k, p->k_stride_b, kss, p->k_stride_h, es) ||
+        !rows_aligned(p->v, p->v_stride_b, vss, p->v_stride_h, es) ||
+        !rows_aligned(p->o, p->o_stride_b, oss, p->o_stride_h, es))
         ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_fwd: every Q/K/V/O row must start on a 16-byte boundary");
+    auto slice_fits = [&](int64_t stride_s, int64_t seq) {
+        return stride_s >= 0 && (seq + 16) * stride_s * es + (int64_t)p->head_dim * es <= 0x7fffffffLL;
+    };
+    if (!slice_fits(qss, p->seq_q) || !slice_fits(oss, p->seq_q) || !slice_fits(kss, p->seq_kv) ||
+        !slice_fits(vss, p->seq_kv))
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_fwd: sequence strides must be >= 0 and one (batch, head) slice < 2 GiB");
+    if (oss < p->head_dim)
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_fwd: output rows overlap (o_stride_s %lld < head_dim %d)",
+                 (long long)p->o_stride_s, p->head_dim);
 
     AttnArgs a;
     a.q = p->q;
     a.k = p->k;
     a.v = p->v;
     a.o = p->o;
-    a.qsb = p->q_stride_b; a.qss = p->q_stride_s; a.qsh = p->q_stride_h;
-    a.ksb = p->k_stride_b; a.kss = p->k_stride_s; a.ksh = p->k_stride_h;
-    a.vsb = p->v_stride_b; a.vss = p->v_stride_s; a.vsh = p->v_stride_h;
-    a.osb = p->o_stride_b; a.oss = p->o_stride_s; a.osh = p->o_stride_h;
+    a.qsb = p->q_stride_b; a.qss = qss; a.qsh = p->q_stride_h;
+    a.ksb = p->k_stride_b; a.kss = kss; a.ksh = p->k_stride_h;
+    a.vsb = p->v_stride_b; a.vss = vss; a.vsh = p->v_stride_h;
+    a.osb = p->o_stride_b; a.oss = oss; a.osh = p->o_stride_h;
     a.kpad = p->key_pad;
     a.kpsb = p->key_pad_stride_b;
     a.H = p->num_heads;

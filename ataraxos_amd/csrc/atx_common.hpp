@@ -41,6 +41,18 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// Streaming variants (nontemporal hint) for data touched exactly once.  On
+// MI355X a streaming store pays off only when each store instruction writes
+// whole 128-byte lines (measured: whole lines 214 us vs 229 us plain for the
+// attention traffic of C3; half lines per instruction 235 us), which is how
+// the attention kernel stages its output rows.
+#ifndef ATX_STREAM_LOADS
+#define ATX_STREAM_LOADS 1
+#endif
+#ifndef ATX_STREAM_STORES
+#define ATX_STREAM_STORES 1
+#endif
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 // 16-bit element types that run on the 16x16x32 MFMA.
@@ -119,6 +131,21 @@ __device__ inline float colgroup_sum(float v) {
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ inline float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
+// Raw buffer access through a per-tensor descriptor (gfx9 dword 3 =
+// 0x00020000).  A load whose offset lies past `bytes` returns zero and such a
+// store is dropped, so tile edges need neither clamps nor predicates.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ inline rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+constexpr int kAuxNt = 2;  // cache-policy bit of the streaming (nontemporal) hint
+__device__ inline u32x4 buf_ld16(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, ATX_STREAM_LOADS ? kAuxNt : 0);
+}
+__device__ inline void buf_st16(rsrc_t r, uint32_t off, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, ATX_STREAM_STORES ? kAuxNt : 0);
+}
+
 // LDS byte pointer.  Kernels address their shared memory through this type so
 // that every access stays a ds_* instruction.
 typedef __attribute__((address_space(3))) char lds_t;
@@ -134,6 +161,18 @@ __device__ inline lds_t* lds_base() {
 __device__ inline lds_t* lds_opaque(lds_t* p) {
     asm volatile("" : "+v"(p));
     return p;
+}
+
+// Hand-off of LDS data between the lanes of one wave.  The hardware runs a
+// wave's LDS instructions in order, so no instruction is needed; but for the
+// compiler, one lane reading what another lane wrote without synchronisation
+// is a data race, and it may keep a value a lane loaded earlier from the same
+// address (or move the read into the writers' branch).  A wavefront-scope
+// fence makes the writes visible to the reads that follow it.
+__device__ inline void wave_lds_handoff() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 __device__ inline u32x4 lds_ld16(const lds_t* p) { return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(p); }
@@ -153,17 +192,7 @@ __device__ inline u32x4 ld16(const void* p) { return *reinterpret_cast<const u32
 __device__ inline void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ inline void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
 
-// Streaming variants (nontemporal hint) for data touched exactly once.  On
-// MI355X a streaming store pays off only when each store instruction writes
-// whole 128-byte lines (measured: whole lines 214 us vs 229 us plain for the
-// attention traffic of C3; half lines per instruction 235 us), which is how
-// the attention kernel stages its output rows.
-#ifndef ATX_STREAM_LOADS
-#define ATX_STREAM_LOADS 1
-#endif
-#ifndef ATX_STREAM_STORES
-#define ATX_STREAM_STORES 1
-#endif
+
 __device__ inline u32x4 ld16_stream(const void* p) {
     if constexpr (ATX_STREAM_LOADS) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
     return ld16(p);

@@ -116,6 +116,9 @@ def test_attention_validation_codes():
     _expect("atx_attn_fwd", _attn_params(seq_kv=257), _lib.ERR_UNSUPPORTED, "seq_kv")
     _expect("atx_attn_fwd", _attn_params(q=(1 << 20) + 8), _lib.ERR_INVALID_ARGUMENT, "16-byte")
     _expect("atx_attn_fwd", _attn_params(k_stride_s=385), _lib.ERR_INVALID_ARGUMENT, "16-byte")
+    _expect("atx_attn_fwd", _attn_params(o_stride_s=32), _lib.ERR_INVALID_ARGUMENT, "overlap")
+    _expect("atx_attn_fwd", _attn_params(k_stride_s=-384), _lib.ERR_UNSUPPORTED, ">= 0")
+    _expect("atx_attn_fwd", _attn_params(v_stride_s=1 << 26), _lib.ERR_UNSUPPORTED, "2 GiB")
 
 
 def test_policy_validation_codes():

@@ -163,6 +163,49 @@ def test_strided_packed_qkv_views(cuda):
     assert_close(out, ref, torch.bfloat16, "packed views")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("sq,skv", [(37, 100), (100, 100), (5, 41), (1, 1)])
+def test_rows_past_the_sequence_are_neither_read_nor_written(cuda, dtype, sq, skv):
+    """Q/K/V/O as the first rows of longer buffers: K/V rows past S_kv and Q
+    rows past S_q hold NaN, the output buffer's rows past S_q hold a sentinel.
+    The result must match the oracle and the sentinel must survive."""
+    _announce(f"guard rows sq={sq} skv={skv} {dtype}")
+    b, h, d, extra = 3, 6, 64, 24
+    q = randn((b, sq, h, d), 51, dtype)
+    k = randn((b, skv, h, d), 52, dtype)
+    v = randn((b, skv, h, d), 53, dtype)
+    nan = float("nan")
+    qb = torch.full((b, sq + extra, h, d), nan, dtype=dtype)
+    kb = torch.full((b, skv + extra, h, d), nan, dtype=dtype)
+    vb = torch.full((b, skv + extra, h, d), nan, dtype=dtype)
+    qb[:, :sq], kb[:, :skv], vb[:, :skv] = q, k, v
+    ob = torch.full((b, sq + extra, h, d), 7.0, dtype=dtype, device=cuda)
+    qb, kb, vb = qb.to(cuda), kb.to(cuda), vb.to(cuda)
+    out = ops.attention_forward(qb[:, :sq], kb[:, :skv], vb[:, :skv], out=ob[:, :sq])
+    torch.cuda.synchronize()
+    assert (ob[:, sq:] == 7.0).all()
+    ref = oracle_attention(to_np64(q), to_np64(k), to_np64(v))
+    assert_close(out, ref, dtype, f"guard rows sq={sq} skv={skv}")
+
+
+def test_single_row_with_arbitrary_sequence_stride(cuda):
+    """A length-1 sequence's stride is meaningless (torch may report any
+    value); the call must not depend on it."""
+    _announce("seq 1 odd strides")
+    b, h, d = 4, 6, 64
+    base = randn((b, h, 3, d), 61, torch.bfloat16)
+    q = base[:, :, 0:1].permute(0, 2, 1, 3)  # [b, 1, h, d], stride_s = d
+    k = base[:, :, 1:2].permute(0, 2, 1, 3)
+    v = base[:, :, 2:3].permute(0, 2, 1, 3)
+    qs, ks, vs = (t.as_strided(t.shape, (t.stride(0), 3, t.stride(2), 1)) for t in (q, k, v))
+    bc = base.to(cuda)
+    gq, gk, gv = (bc[:, :, i : i + 1].permute(0, 2, 1, 3) for i in range(3))
+    gq, gk, gv = (t.as_strided(t.shape, (t.stride(0), 3, t.stride(2), 1), t.storage_offset()) for t in (gq, gk, gv))
+    out = ops.attention_forward(gq, gk, gv)
+    ref = oracle_attention(to_np64(qs), to_np64(ks), to_np64(vs))
+    assert_close(out, ref, torch.bfloat16, "seq 1")
+
+
 def test_determinism(cuda):
     q = randn((8, 100, 6, 64), 1, torch.bfloat16).to(cuda)
     k = randn((8, 100, 6, 64), 2, torch.bfloat16).to(cuda)
