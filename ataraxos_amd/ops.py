@@ -95,7 +95,9 @@ def attention_forward(
         if tuple(key_padding_mask.shape) != (b, skv):
             raise ValueError(f"attention: key_padding_mask must be [{b}, {skv}]")
         _require_device("attention", q, key_padding_mask)
-        pad = key_padding_mask.to(torch.uint8).contiguous()
+        # bool and uint8 share one byte per element: reinterpret, no copy
+        pad = (key_padding_mask.view(torch.uint8) if key_padding_mask.dtype == torch.bool
+               else (key_padding_mask != 0).view(torch.uint8)).contiguous()
     if scale is None:
         scale = 1.0 / math.sqrt(d)
 

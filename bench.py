@@ -21,6 +21,9 @@ roofline = 18.2 M samples/s).  Also reported on the same line:
 * ``e2e``: the full MultiHeadAttention forward of the 8 layers (QKV
   projections, attention, output projection, residual);
 * ``kq_policy``: the fused key-query policy kernel at config C2;
+* ``belief_attention``: the attention kernel at the config C4 shapes
+  (encoder self, decoder causal self, decoder cross with key padding);
+* ``decode``: the KV-cache decode kernel over config C5's 4 layers x 40 steps;
 * ``cpu_baseline``: the reference's math path (torch on the host CPU) on a
   bounded sample of the same layer, rank 0 only.
 
@@ -56,7 +59,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--qkv", choices=("separate", "packed"), default="separate",
                     help="q/k/v as three tensors or as views of one fused [B, L, 3E] projection")
-    ap.add_argument("--no-extras", action="store_true", help="skip the e2e and kq_policy legs")
+    ap.add_argument("--no-extras", action="store_true", help="skip the e2e, kq_policy, belief_attention and decode legs")
     ap.add_argument("--cpu-sample", type=int, default=1024, help="batch of the CPU baseline sample")
     ap.add_argument(
         "--mode",
@@ -175,16 +178,7 @@ def time_kq(torch, ops, batch, dev, steps, warmup):
     mask = torch.rand(batch, s, s, generator=g, device=dev) < 0.02
     mask[:, 0, 0] |= ~mask.flatten(1).any(dim=1)
     out = torch.empty(batch, s * s, dtype=torch.float32, device=dev)
-    for _ in range(warmup):
-        ops.kq_policy(q, k, mask, out=out)
-    torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    for i in range(steps):
-        ev[i].record()
-        ops.kq_policy(q, k, mask, out=out)
-    ev[steps].record()
-    torch.cuda.synchronize()
-    ms = sum(ev[i].elapsed_time(ev[i + 1]) for i in range(steps)) / steps
+    ms = _mean_launch_ms(torch, lambda: ops.kq_policy(q, k, mask, out=out), steps, warmup)
     bytes_per_sample = 2 * s * d * 2 + s * s + s * s * 4
     return {
         "config": "C2 KQ logits + legal mask + softmax, B=4096, 100x100, d=64, bf16 in, fp32 out",
@@ -193,6 +187,109 @@ def time_kq(torch, ops, batch, dev, steps, warmup):
         "achieved_gbs": batch * bytes_per_sample / (ms * 1e-3) / 1e9,
         "hbm_frac": batch * bytes_per_sample / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
     }
+
+
+def _mean_launch_ms(torch, fn, steps, warmup):
+    """Mean duration of ``fn()`` (one kernel launch) over ``steps`` calls,
+    from events recorded on the current stream around each call.  A GPU-side
+    spin queued first lets the host enqueue every call before the GPU reaches
+    them, so host launch overhead of short kernels does not enter the times."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    if hasattr(torch.cuda, "_sleep"):
+        torch.cuda._sleep(20_000_000)  # ~10 ms of clock cycles
+    for i in range(steps):
+        ev[i].record()
+        fn()
+    ev[steps].record()
+    torch.cuda.synchronize()
+    return sum(ev[i].elapsed_time(ev[i + 1]) for i in range(steps)) / steps
+
+
+def _leg(what, ms, nbytes, samples):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"what": what, "kernel_us": ms * 1e3, "achieved_gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+            "samples_per_s": samples / (ms * 1e-3)}
+
+
+def time_belief(torch, ops, dev, steps, warmup):
+    """Config C4 attention shapes, B=2048, 8 heads x 64, bf16: encoder
+    self-attention (L=100), decoder causal self-attention (40 tokens), decoder
+    cross-attention 40 -> 100 with all keys valid and with a Bernoulli(0.4)
+    key-padding mask (>= 1 valid key per sample)."""
+    g = torch.Generator(device=dev).manual_seed(46)
+    b, h, d, e = 2048, 8, 64, 512
+
+    def bshd(s):
+        return torch.randn(b, s, e, generator=g, device=dev).to(torch.bfloat16).view(b, s, h, d)
+
+    enc = [bshd(100) for _ in range(3)]
+    dec = [bshd(40) for _ in range(3)]
+    pad = torch.rand(b, 100, generator=g, device=dev) < 0.4
+    pad[:, 0] &= pad[:, 1:].all(dim=1).logical_not()  # keep key 0 valid where all others are padded
+    o100, o40 = torch.empty_like(enc[0]), torch.empty_like(dec[0])
+    row = e * 2  # bytes of one token's Q, K, V or O row
+    legs = {
+        "encoder_self_L100": _leg(
+            "encoder self-attention, S=100", _mean_launch_ms(torch, lambda: ops.attention_forward(*enc, out=o100), steps, warmup),
+            b * 100 * row * 4, b),
+        "decoder_self_causal_L40": _leg(
+            "decoder causal self-attention, S=40",
+            _mean_launch_ms(torch, lambda: ops.attention_forward(*dec, causal=True, out=o40), steps, warmup),
+            b * 40 * row * 4, b),
+        "decoder_cross_40x100": _leg(
+            "decoder cross-attention 40 -> 100",
+            _mean_launch_ms(torch, lambda: ops.attention_forward(dec[0], enc[1], enc[2], out=o40), steps, warmup),
+            b * (40 * 2 + 100 * 2) * row, b),
+        "decoder_cross_40x100_keypad": _leg(
+            "decoder cross-attention 40 -> 100, Bernoulli(0.4) key padding",
+            _mean_launch_ms(torch, lambda: ops.attention_forward(dec[0], enc[1], enc[2], key_padding_mask=pad, out=o40),
+                            steps, warmup),
+            b * (40 * 2 + 100 * 2) * row + b * 100, b),
+    }
+    total_us = 6 * legs["encoder_self_L100"]["kernel_us"] + 4 * (
+        legs["decoder_self_causal_L40"]["kernel_us"] + legs["decoder_cross_40x100_keypad"]["kernel_us"])
+    return {"config": "C4 Belief-net attention, B=2048, 8x64, bf16", "legs": legs,
+            "attention_us_per_forward": total_us,
+            "note": "attention_us_per_forward = 6 encoder layers + 4 decoder layers (causal self + padded cross)"}
+
+
+def time_decode(torch, ops, dev, reps):
+    """Config C5: B=8192, 8 heads x 64, bf16, 4 layers x 40 steps; step t
+    appends the new K/V row to each layer's [B, 8, 40, 64] cache and attends
+    over t rows.  Whole 160-launch sequence timed, ``reps`` times."""
+    g = torch.Generator(device=dev).manual_seed(47)
+    b, h, d, t_max, n_layers = 8192, 8, 64, 40, 4
+    caches = [(torch.zeros(b, h, t_max, d, dtype=torch.bfloat16, device=dev),
+               torch.zeros(b, h, t_max, d, dtype=torch.bfloat16, device=dev)) for _ in range(n_layers)]
+    step_in = [tuple(torch.randn(b, h, d, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+               for _ in range(n_layers)]
+    out = torch.empty(b, h, d, dtype=torch.bfloat16, device=dev)
+
+    def sequence():
+        for t in range(1, t_max + 1):
+            for (kc, vc), (q, kn, vn) in zip(caches, step_in):
+                ops.attention_decode(q, kc, vc, t, kn, vn, out=out)
+
+    sequence()
+    torch.cuda.synchronize()
+    a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        sequence()
+    z.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(z) / reps
+    e = h * d
+    # per layer-step: K/V rows 0..t-1 read (the new row from k_new / v_new),
+    # the new rows written to the caches, q read, o written
+    nbytes = sum(n_layers * (2 * b * h * t * d * 2 + 2 * b * e * 2 + 2 * b * e * 2) for t in range(1, t_max + 1))
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"config": "C5 Setup-net decode, B=8192, 8x64, bf16, 4 layers x 40 steps",
+            "ms_per_sequence": ms, "launches": t_max * n_layers, "us_per_launch": ms * 1e3 / (t_max * n_layers),
+            "achieved_gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "bytes_per_sequence": nbytes}
 
 
 def cpu_baseline(sample: int) -> dict:
@@ -308,6 +405,8 @@ def main() -> int:
             "attention_share": (ms_step / e2e_ms) if e2e_ms > 0 else None,
         }
         result["kq_policy"] = time_kq(torch, ops, batch, dev, args.steps, args.warmup)
+        result["belief_attention"] = time_belief(torch, ops, dev, args.steps, args.warmup)
+        result["decode"] = time_decode(torch, ops, dev, max(3, args.steps // 10))
         print("[bench] extras timed", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_sample)
