@@ -145,6 +145,14 @@ __device__ inline u32x4 buf_ld16(rsrc_t r, uint32_t off) {
 __device__ inline void buf_st16(rsrc_t r, uint32_t off, u32x4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, ATX_STREAM_STORES ? kAuxNt : 0);
 }
+// Stores without the streaming hint (L2 keeps the line and merges the
+// pieces of partly written lines before writing back).
+__device__ inline void buf_st16_cached(rsrc_t r, uint32_t off, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, 0);
+}
+__device__ inline void buf_st4_cached(rsrc_t r, uint32_t off, uint32_t v) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, (int)off, 0, 0);
+}
 
 // LDS byte pointer.  Kernels address their shared memory through this type so
 // that every access stays a ds_* instruction.
@@ -186,6 +194,10 @@ __device__ inline u32x2 lds_ld8_tr16(const lds_t* p) {
     return __builtin_bit_cast(u32x2, v);
 }
 __device__ inline void lds_st8(lds_t* p, u32x2 v) { *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(p) = v; }
+__device__ inline uint32_t lds_ld4(const lds_t* p) { return *reinterpret_cast<const __attribute__((address_space(3))) uint32_t*>(p); }
+__device__ inline void lds_st4(lds_t* p, uint32_t v) { *reinterpret_cast<__attribute__((address_space(3))) uint32_t*>(p) = v; }
+__device__ inline uint32_t lds_ld1(const lds_t* p) { return *reinterpret_cast<const __attribute__((address_space(3))) uint8_t*>(p); }
+__device__ inline void lds_st1(lds_t* p, uint32_t v) { *reinterpret_cast<__attribute__((address_space(3))) uint8_t*>(p) = (uint8_t)v; }
 
 // 16-byte global load / store through the vector memory path.
 __device__ inline u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }

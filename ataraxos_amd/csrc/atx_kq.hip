@@ -9,10 +9,12 @@
 //
 // Layout: the S x S logits of one sample are computed as 16x16 MFMA tiles of
 // L^T = K Q^T, so lane (m, g) of a tile holds from-square 16*it + m against
-// the four consecutive to-squares 16*jt + 4g .. +3: one 16-byte fp32 store and
-// one 4-byte mask load per tile and lane.  The whole sample (<= 128 x 128
-// logits) stays in registers across the two block reductions (max, sum), so
-// the logits are never written to memory.
+// the four consecutive to-squares 16*jt + 4g .. +3.  The four waves of a
+// workgroup split the tile rows and keep their logits in registers across
+// the two block reductions (max, sum), so the logits are never written to
+// memory.  LDS holds first the K and Q rows of a 128-byte feature slice and
+// the sample's legality bytes, then the finished S*S fp32 row, which leaves
+// as one contiguous run of 16-byte stores.
 #include "atx_common.hpp"
 
 namespace atx {
@@ -25,252 +27,320 @@ struct KqArgs {
     int64_t msb, mss;
     float* out;
     int64_t osb;
-    int S, nchunks;  // nchunks: 16-byte chunks per q/k row
+    int B, S, nchunks;  // nchunks: 16-byte chunks per q/k row
     float scale, c2;
     int probs;
-    int mask_vec;  // 4-byte mask loads are aligned
-    int out_vec;   // 16-byte output stores are aligned
+    int mask_lin;  // a sample's legality bytes are S*S contiguous bytes, 16-byte aligned, S % 4 == 0
+    int out_vec;   // a sample's output starts 16-byte aligned and S*S % 4 == 0
 };
 
 namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-constexpr int kSliceChunks = 8;            // 16-byte chunks per staged slice
-constexpr int kRowBytes = kSliceChunks * 16 + 16;  // padded LDS row (odd number of 16B units)
+constexpr int kSliceChunks = 8;  // 16-byte chunks per staged slice = one 128-byte LDS row
 
+// One 128-byte feature slice of a 16x16 tile: two 16-byte operand chunks per
+// lane for each of A (K rows) and B (Q rows).
 template <typename T>
-struct KqMma;
-
-template <>
-struct KqMma<__bf16> {
-    __device__ static inline f32x4 slice(const char* krow, const char* qrow, int g, f32x4 acc) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const u32x4 a = *reinterpret_cast<const u32x4*>(krow + (4 * i + g) * 16);
-            const u32x4 b = *reinterpret_cast<const u32x4*>(qrow + (4 * i + g) * 16);
-            acc = Mfma16<__bf16>::mma(a, b, acc);
-        }
-        return acc;
-    }
-};
-
-template <>
-struct KqMma<_Float16> {
-    __device__ static inline f32x4 slice(const char* krow, const char* qrow, int g, f32x4 acc) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const u32x4 a = *reinterpret_cast<const u32x4*>(krow + (4 * i + g) * 16);
-            const u32x4 b = *reinterpret_cast<const u32x4*>(qrow + (4 * i + g) * 16);
-            acc = Mfma16<_Float16>::mma(a, b, acc);
-        }
-        return acc;
+struct KqMma {
+    __device__ static inline f32x4 slice(const u32x4 (&a)[2], const u32x4 (&b)[2], f32x4 acc) {
+        acc = Mfma16<T>::mma(a[0], b[0], acc);
+        return Mfma16<T>::mma(a[1], b[1], acc);
     }
 };
 
 template <>
 struct KqMma<float> {
-    __device__ static inline f32x4 slice(const char* krow, const char* qrow, int g, f32x4 acc) {
+    __device__ static inline f32x4 slice(const u32x4 (&a)[2], const u32x4 (&b)[2], f32x4 acc) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const f32x4 a = as_f32x4(*reinterpret_cast<const u32x4*>(krow + (4 * i + g) * 16));
-            const f32x4 b = as_f32x4(*reinterpret_cast<const u32x4*>(qrow + (4 * i + g) * 16));
+            const f32x4 fa = as_f32x4(a[i]), fb = as_f32x4(b[i]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc = mma_f32(a[j], b[j], acc);
+            for (int j = 0; j < 4; ++j) acc = mma_f32(fa[j], fb[j], acc);
         }
         return acc;
     }
 };
 
-__device__ inline float wave_max(float v) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, shfl_xor(v, off));
-    return v;
-}
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) v += shfl_xor(v, off);
-    return v;
-}
-
 }  // namespace
 
-// NT = number of 16-square tiles per side (S <= 16*NT).
-template <typename T, int NT>
-__global__ __launch_bounds__(kThreads) void kq_policy(KqArgs a) {
-    constexpr int NTILE = NT * NT;
-    constexpr int TPW = (NTILE + kWaves - 1) / kWaves;
-    constexpr int ROWS = NT * 16;
+// LDS bytes for one workgroup: the K and Q rows of one 128-byte feature slice
+// plus the legality bytes [S][SP] (SP = S rounded up to 4), or the finished
+// values [S][SP] fp32, whichever is larger (they reuse one region).
+inline int kq_lds_bytes(int nt, int S) {
+    const int SP = (S + 3) & ~3;
+    const int staged = 2 * nt * 16 * 128 + ((S * SP + 15) & ~15);
+    const int out = S * SP * 4;
+    return staged > out ? staged : out;
+}
 
-    __shared__ __attribute__((aligned(16))) char sq[ROWS * kRowBytes];
-    __shared__ __attribute__((aligned(16))) char sk[ROWS * kRowBytes];
+// One workgroup per sample; NT = number of 16-square tiles per side
+// (S <= 16*NT); MULTI = features wider than one 128-byte slice; PROBS =
+// softmax output (else masked logits).
+//
+// Wave w owns the tile rows it = w, w + 4, ... (R of them) and every tile
+// column jt, and keeps their logits in registers (tile (r, jt) of the wave
+// in acc[r][jt]).  The max and the sum of the softmax are reduced as trees
+// in registers, then across the waves; the finished values go through LDS
+// so that the sample's S*S row leaves as contiguous 16-byte stores.
+template <typename T, int NT, bool MULTI, bool PROBS>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(MULTI ? 2 : 4, 8)))
+void kq_policy(KqArgs a) {
+    constexpr int R = (NT + kWaves - 1) / kWaves;
+    constexpr int ROWS = NT * 16;
+    constexpr int QKC = ROWS * kSliceChunks;               // chunks per tensor and slice
+    constexpr int QIT = (QKC + kThreads - 1) / kThreads;   // per thread
+    constexpr int MIT = (ROWS * ROWS / 16 + kThreads - 1) / kThreads;  // legality chunks per thread
+    constexpr int NLB = (R * NT * 4 + 31) / 32;
+
+    lds_t* const sk = lds_base();
+    lds_t* const sq = sk + ROWS * 128;
+    lds_t* const smask = sq + ROWS * 128;
+    lds_t* const sout = sk;  // after the products and the legality reads
     __shared__ float red[kWaves];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: tile rows stay scalar
     const int m = lane & 15, g = lane >> 4;
     const int b = blockIdx.x;
     const int S = a.S;
-
-    const char* qb = static_cast<const char*>(a.q) + (int64_t)b * a.qsb * sizeof(T);
-    const char* kb = static_cast<const char*>(a.k) + (int64_t)b * a.ksb * sizeof(T);
-    const int64_t qrs = a.qss * (int64_t)sizeof(T), krs = a.kss * (int64_t)sizeof(T);
-
-    // ---- legality bytes, fetched before the products -------------------
-    uint32_t mbits[TPW];
-#pragma unroll
-    for (int u = 0; u < TPW; ++u) {
-        const int t = wave + kWaves * u;
-        const int it = t / NT, jt = t - (t / NT) * NT;
-        const int i = it * 16 + m, j0 = jt * 16 + 4 * g;
-        uint32_t w = 0;
-        if (t < NTILE && i < S && j0 < S) {
-            if (!a.mask) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (j0 + e < S) w |= 1u << (8 * e);
-            } else {
-                const uint8_t* mrow = a.mask + (int64_t)b * a.msb + (int64_t)i * a.mss;
-                if (a.mask_vec) {
-                    w = *reinterpret_cast<const uint32_t*>(mrow + j0);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (j0 + e < S) w |= (uint32_t)(mrow[j0 + e] != 0) << (8 * e);
-                }
-            }
-        }
-        mbits[u] = w;
-    }
-
-    // ---- logits: loop over 8-chunk slices of the feature dimension --------
-    f32x4 acc[TPW];
-#pragma unroll
-    for (int u = 0; u < TPW; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    for (int sc = 0; sc < a.nchunks; sc += kSliceChunks) {
-        if (sc) __syncthreads();
-        for (int idx = tid; idx < S * kSliceChunks; idx += kThreads) {
-            const int r = idx >> 3, c = idx & 7;
-            const bool in = sc + c < a.nchunks;
-            const u32x4 qv = in ? ld16(qb + r * qrs + (sc + c) * 16) : u32x4{0, 0, 0, 0};
-            const u32x4 kv = in ? ld16(kb + r * krs + (sc + c) * 16) : u32x4{0, 0, 0, 0};
-            *reinterpret_cast<u32x4*>(sq + r * kRowBytes + c * 16) = qv;
-            *reinterpret_cast<u32x4*>(sk + r * kRowBytes + c * 16) = kv;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int u = 0; u < TPW; ++u) {
-            const int t = wave + kWaves * u;
-            if (t < NTILE) {
-                const int it = t / NT, jt = t - (t / NT) * NT;
-                acc[u] = KqMma<T>::slice(sk + (jt * 16 + m) * kRowBytes, sq + (it * 16 + m) * kRowBytes, g, acc[u]);
-            }
-        }
-    }
-
-    float* ob = a.out + (int64_t)b * a.osb;
+    const int SP = (S + 3) & ~3;
+    const int nslices = (a.nchunks + kSliceChunks - 1) / kSliceChunks;
+    constexpr int es = sizeof(T);
+    const uint32_t row_bytes = (uint32_t)a.nchunks * 16;
+    const uint32_t qrs = (uint32_t)(a.qss * es), krs = (uint32_t)(a.kss * es);
+    // rows past S read as zero: the descriptors end at the last row
+    const rsrc_t rq = make_rsrc(static_cast<const T*>(a.q) + b * a.qsb, (uint32_t)((S - 1) * a.qss * es) + row_bytes);
+    const rsrc_t rk = make_rsrc(static_cast<const T*>(a.k) + b * a.ksb, (uint32_t)((S - 1) * a.kss * es) + row_bytes);
     const float kNegInf = -__builtin_inff();
 
-    if (!a.probs) {
+    // ---- slice sc of Q and K (and, with the first, the legality bytes) ->
+    //      LDS.  Chunk c of row r sits at c ^ ((r >> 1) & 7): the 16 rows one
+    //      MFMA operand read touches fall in distinct bank groups. ----------
+    auto stage = [&](int sc) {
+        u32x4 qv[QIT], kv[QIT], mv[MIT];
 #pragma unroll
-        for (int u = 0; u < TPW; ++u) {
-            const int t = wave + kWaves * u;
-            const int it = t / NT, jt = t - (t / NT) * NT;
-            const int i = it * 16 + m, j0 = jt * 16 + 4 * g;
-            if (t < NTILE && i < S && j0 < S) {
-                float r[4];
+        for (int it = 0; it < QIT; ++it) {
+            const uint32_t idx = tid + it * kThreads;
+            const uint32_t r = idx >> 3, c = sc * kSliceChunks + (idx & 7);
+            const bool in = (int)c < a.nchunks;
+            qv[it] = in ? buf_ld16(rq, r * qrs + c * 16) : u32x4{0, 0, 0, 0};
+            kv[it] = in ? buf_ld16(rk, r * krs + c * 16) : u32x4{0, 0, 0, 0};
+        }
+        const bool lin = sc == 0 && a.mask && a.mask_lin;
+        if (lin) {
+            const rsrc_t rm = make_rsrc(a.mask + b * a.msb, (uint32_t)(S * S));
 #pragma unroll
-                for (int e = 0; e < 4; ++e) r[e] = ((mbits[u] >> (8 * e)) & 0xff) ? acc[u][e] * a.scale : -1e10f;
-                float* dst = ob + (int64_t)i * S + j0;
-                if (a.out_vec) {
-                    st16(dst, __builtin_bit_cast(u32x4, f32x4{r[0], r[1], r[2], r[3]}));
-                } else {
+            for (int it = 0; it < MIT; ++it) mv[it] = buf_ld16(rm, (tid + it * kThreads) * 16);  // past S*S: zero
+        }
+        if (sc) __syncthreads();  // the previous slice's operand reads are done
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (j0 + e < S) dst[e] = r[e];
-                }
+        for (int it = 0; it < QIT; ++it) {
+            const uint32_t idx = tid + it * kThreads;
+            if (QKC % kThreads == 0 || idx < QKC) {
+                const uint32_t r = idx >> 3, c = idx & 7;
+                const uint32_t pc = (c ^ ((r >> 1) & 7)) << 4;
+                lds_st16(sq + r * 128 + pc, qv[it]);
+                lds_st16(sk + r * 128 + pc, kv[it]);
             }
         }
-        return;
+        if (lin) {  // SP == S: one contiguous run
+#pragma unroll
+            for (int it = 0; it < MIT; ++it) {
+                const int idx = tid + it * kThreads;
+                if (idx * 16 < S * S) lds_st16(smask + idx * 16, mv[it]);
+            }
+        } else if (sc == 0) {  // any layout, or no mask (= every square legal)
+            const uint8_t* mb = a.mask ? a.mask + b * a.msb : nullptr;
+            for (int idx = tid; idx < S * SP; idx += kThreads) {
+                const int i = idx / SP, j = idx - i * SP;
+                uint32_t v = j < S;
+                if (mb && j < S) v = mb[i * a.mss + j] != 0;
+                lds_st1(smask + idx, v);
+            }
+        }
+        __syncthreads();
+    };
+
+    // ---- logits of the wave's tiles.  Lane (m, g) supplies chunks g and
+    //      4 + g of row 16*t + m (the swizzle of those rows depends on m
+    //      only).  Rows past the board (it >= NT) repeat the last tile row;
+    //      their legality is zero. ---------------------------------------
+    const int sw = (m >> 1) & 7;
+    const int c0 = (g ^ sw) * 16, c1 = ((4 + g) ^ sw) * 16;
+    f32x4 acc[R][NT];
+    auto products = [&](bool first) {
+        u32x4 qop[R][2];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const lds_t* qrow = sq + (min(wave + kWaves * r, NT - 1) * 16 + m) * 128;
+            qop[r][0] = lds_ld16(qrow + c0);
+            qop[r][1] = lds_ld16(qrow + c1);
+        }
+        const lds_t* krow = lds_opaque(sk + m * 128);
+#pragma unroll
+        for (int jt = 0; jt < NT; ++jt) {
+            const u32x4 kop[2] = {lds_ld16(krow + jt * 2048 + c0), lds_ld16(krow + jt * 2048 + c1)};
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                acc[r][jt] = KqMma<T>::slice(kop, qop[r], first ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[r][jt]);
+            // one tile column at a time: the scheduler may not hoist the
+            // operand reads of every column (their registers would spill)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    if constexpr (!MULTI) {
+        stage(0);
+        products(true);
+    } else {
+        for (int sc = 0; sc < nslices; ++sc) {
+            stage(sc);
+            products(sc == 0);
+        }
     }
 
-    // ---- softmax over the S*S legal entries ------------------------------
-    float mx = kNegInf;
+    // ---- legality, 4 bits per tile (bit 4u + e = to-square 4g + e of tile
+    //      u = r*NT + jt), from a word of 4 bytes read at a clamped address;
+    //      cleared off the board --------------------------------------------
+    uint32_t lbits[NLB] = {};
 #pragma unroll
-    for (int u = 0; u < TPW; ++u)
+    for (int r = 0; r < R; ++r) {
+        const int i = (wave + kWaves * r) * 16 + m;  // >= S also covers it >= NT
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if ((mbits[u] >> (8 * e)) & 0xff) mx = fmaxf(mx, acc[u][e]);
-    mx = wave_max(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-
-    const bool none_legal = (mx == kNegInf);
-    const float mb = mx * a.c2;
-    float lsum = 0.f;
-#pragma unroll
-    for (int u = 0; u < TPW; ++u)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const bool legal = (mbits[u] >> (8 * e)) & 0xff;
-            const float p = legal ? fast_exp2(__builtin_fmaf(acc[u][e], a.c2, -mb)) : 0.f;
-            acc[u][e] = p;
-            lsum += p;
+        for (int jt = 0; jt < NT; ++jt) {
+            const int j0 = jt * 16 + 4 * g;
+            uint32_t w = lds_ld4(smask + min(i, S - 1) * SP + min(j0, SP - 4));
+            w |= w >> 4;  // fold each byte onto its bit 0
+            w |= w >> 2;
+            w |= w >> 1;
+            uint32_t nib = (w & 1u) | ((w >> 7) & 2u) | ((w >> 14) & 4u) | ((w >> 21) & 8u);
+            if (!(i < S && j0 < S)) nib = 0;
+            const int u = r * NT + jt;
+            lbits[u / 8] |= nib << (4 * (u % 8));
         }
-    lsum = wave_sum(lsum);
-    if (lane == 0) red[wave] = lsum;
-    __syncthreads();
-    lsum = (red[0] + red[1]) + (red[2] + red[3]);
-    const float inv = 1.0f / lsum;
-    const float uniform = 1.0f / (float)(S * S);
+    }
 
+    // ---- values.  Softmax: logits scaled by scale*log2(e), illegal -> -inf;
+    //      exp2(x - max) makes the maximum exactly 1 (a single legal move gets
+    //      probability exactly 1).  Logits: scaled, illegal -> -1e10. --------
+    const float mul = PROBS ? a.c2 : a.scale;
+    const float fill = PROBS ? kNegInf : -1e10f;
 #pragma unroll
-    for (int u = 0; u < TPW; ++u) {
-        const int t = wave + kWaves * u;
-        const int it = t / NT, jt = t - (t / NT) * NT;
-        const int i = it * 16 + m, j0 = jt * 16 + 4 * g;
-        if (t < NTILE && i < S && j0 < S) {
-            float r[4];
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) r[e] = none_legal ? uniform : acc[u][e] * inv;
-            float* dst = ob + (int64_t)i * S + j0;
-            if (a.out_vec) {
-                st16(dst, __builtin_bit_cast(u32x4, f32x4{r[0], r[1], r[2], r[3]}));
-            } else {
+        for (int jt = 0; jt < NT; ++jt) {
+            const int u = r * NT + jt;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (j0 + e < S) dst[e] = r[e];
+            for (int e = 0; e < 4; ++e)
+                acc[r][jt][e] = ((lbits[u / 8] >> (4 * (u % 8) + e)) & 1u) ? acc[r][jt][e] * mul : fill;
+        }
+
+    if constexpr (PROBS) {
+        // per-lane trees, then the wave, then the workgroup
+        float t[R * NT];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int jt = 0; jt < NT; ++jt)
+                t[r * NT + jt] = fmaxf(fmaxf(acc[r][jt][0], acc[r][jt][1]), fmaxf(acc[r][jt][2], acc[r][jt][3]));
+#pragma unroll
+        for (int n = R * NT; n > 1; n = (n + 1) / 2)
+#pragma unroll
+            for (int i = 0; i < n / 2; ++i) t[i] = fmaxf(t[i], t[n - 1 - i]);
+        float mx = t[0];
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) mx = fmaxf(mx, shfl_xor(mx, off));
+        if (lane == 0) red[wave] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        __syncthreads();
+        const bool none_legal = mx == kNegInf;
+        const float base = none_legal ? 0.f : mx;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int jt = 0; jt < NT; ++jt) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[r][jt][e] = fast_exp2(acc[r][jt][e] - base);
+                t[r * NT + jt] = (acc[r][jt][0] + acc[r][jt][1]) + (acc[r][jt][2] + acc[r][jt][3]);
             }
+#pragma unroll
+        for (int n = R * NT; n > 1; n = (n + 1) / 2)
+#pragma unroll
+            for (int i = 0; i < n / 2; ++i) t[i] += t[n - 1 - i];
+        float sm = t[0];
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) sm += shfl_xor(sm, off);
+        if (lane == 0) red[wave] = sm;
+        __syncthreads();
+        sm = (red[0] + red[1]) + (red[2] + red[3]);
+        const float inv = 1.0f / sm;
+        const float uniform = 1.0f / (float)(S * S);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int jt = 0; jt < NT; ++jt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[r][jt][e] = none_legal ? uniform : acc[r][jt][e] * inv;
+    } else {
+        __syncthreads();  // every wave is done with the operand and legality LDS
+    }
+
+    // ---- registers -> LDS [S][SP] -> the sample's contiguous S*S row ------
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = (wave + kWaves * r) * 16 + m;
+        if (i < S) {
+            lds_t* orow = sout + (i * SP + 4 * g) * 4;
+#pragma unroll
+            for (int jt = 0; jt < NT; ++jt)
+                if (jt * 16 + 4 * g < S) lds_st16(orow + jt * 64, __builtin_bit_cast(u32x4, acc[r][jt]));
+        }
+    }
+    __syncthreads();
+    const rsrc_t ro = make_rsrc(a.out + b * a.osb, (uint32_t)(S * S * 4));
+    if (a.out_vec && SP == S) {  // plain (L2-cached) stores: measured faster here than streaming ones
+        for (int idx = tid; idx * 4 < S * S; idx += kThreads) buf_st16_cached(ro, idx * 16, lds_ld16(sout + idx * 16));
+    } else {
+        for (int idx = tid; idx < S * S; idx += kThreads) {
+            const int i = idx / S, j = idx - i * S;
+            buf_st4_cached(ro, idx * 4, lds_ld4(sout + (i * SP + j) * 4));
         }
     }
 }
 
 namespace {
 
-template <typename T>
-int dispatch_kq(int nt, int grid, hipStream_t st, const KqArgs& a) {
-    switch (nt) {
-#define ATX_KQ_CASE(N)                                                             \
-    case N:                                                                        \
-        hipLaunchKernelGGL((kq_policy<T, N>), dim3(grid), dim3(kThreads), 0, st, a); \
-        break;
-        ATX_KQ_CASE(1)
-        ATX_KQ_CASE(2)
-        ATX_KQ_CASE(3)
-        ATX_KQ_CASE(4)
-        ATX_KQ_CASE(5)
-        ATX_KQ_CASE(6)
-        ATX_KQ_CASE(7)
-        ATX_KQ_CASE(8)
-#undef ATX_KQ_CASE
-        default:
-            ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_masked_softmax_fwd: %d tiles", nt);
-    }
+template <typename T, int NT, bool MULTI>
+int launch_kq(hipStream_t st, const KqArgs& a) {
+    if (a.probs)
+        hipLaunchKernelGGL((kq_policy<T, NT, MULTI, true>), dim3(a.B), dim3(kThreads), kq_lds_bytes(NT, a.S), st, a);
+    else
+        hipLaunchKernelGGL((kq_policy<T, NT, MULTI, false>), dim3(a.B), dim3(kThreads), kq_lds_bytes(NT, a.S), st, a);
     ATX_CHECK_LAUNCH("atx_kq_masked_softmax_fwd launch");
     return ATX_OK;
+}
+
+template <typename T, bool MULTI>
+int dispatch_kq_nt(int nt, hipStream_t st, const KqArgs& a) {
+    switch (nt) {
+        case 1: return launch_kq<T, 1, MULTI>(st, a);
+        case 2: return launch_kq<T, 2, MULTI>(st, a);
+        case 3: return launch_kq<T, 3, MULTI>(st, a);
+        case 4: return launch_kq<T, 4, MULTI>(st, a);
+        case 5: return launch_kq<T, 5, MULTI>(st, a);
+        case 6: return launch_kq<T, 6, MULTI>(st, a);
+        case 7: return launch_kq<T, 7, MULTI>(st, a);
+        case 8: return launch_kq<T, 8, MULTI>(st, a);
+        default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_masked_softmax_fwd: %d tiles", nt);
+    }
+}
+
+template <typename T>
+int dispatch_kq(int nt, hipStream_t st, const KqArgs& a) {
+    return a.nchunks > kSliceChunks ? dispatch_kq_nt<T, true>(nt, st, a) : dispatch_kq_nt<T, false>(nt, st, a);
 }
 
 }  // namespace
@@ -304,6 +374,16 @@ extern "C" int atx_kq_masked_softmax_fwd(const AtxKqParams* p, void* stream) {
     if (((uintptr_t)p->out & 3) != 0 || p->out_stride_b < (int64_t)p->seq * p->seq)
         ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_kq_masked_softmax_fwd: out must be 4-byte aligned with stride >= seq*seq");
 
+    if (p->mask && (p->mask_stride_s < 0 || p->mask_stride_b < 0 ||
+                    (int64_t)(p->seq + 16) * p->mask_stride_s + 256 > 0x7fffffffLL))
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_masked_softmax_fwd: mask strides must be >= 0 and one sample < 2 GiB");
+    // One sample's q / k rows are addressed with 32-bit byte offsets.
+    const int64_t row_bytes = (int64_t)p->dim * es;
+    if (p->q_stride_s < 0 || p->k_stride_s < 0 ||
+        (int64_t)(p->seq + 16) * p->q_stride_s * es + row_bytes > 0x7fffffffLL ||
+        (int64_t)(p->seq + 16) * p->k_stride_s * es + row_bytes > 0x7fffffffLL)
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_masked_softmax_fwd: row strides must be >= 0 and one sample < 2 GiB");
+
     KqArgs a;
     a.q = p->q;
     a.k = p->k;
@@ -313,19 +393,20 @@ extern "C" int atx_kq_masked_softmax_fwd(const AtxKqParams* p, void* stream) {
     a.msb = p->mask_stride_b; a.mss = p->mask_stride_s;
     a.out = p->out;
     a.osb = p->out_stride_b;
+    a.B = p->batch;
     a.S = p->seq;
     a.nchunks = p->dim * es / 16;
     a.scale = p->scale;
     a.c2 = p->scale * kLog2e;
     a.probs = p->out_mode == ATX_KQ_OUT_PROBS;
-    a.mask_vec = p->mask && (((uintptr_t)p->mask & 3) == 0) && (p->mask_stride_b % 4 == 0) &&
-                 (p->mask_stride_s % 4 == 0) && (p->seq % 4 == 0);
-    a.out_vec = aligned16(p->out) && (p->out_stride_b % 4 == 0) && (p->seq % 4 == 0);
+    a.mask_lin = p->mask && aligned16(p->mask) && (p->mask_stride_b % 16 == 0) && (p->mask_stride_s == p->seq) &&
+                 (p->seq % 4 == 0);
+    a.out_vec = aligned16(p->out) && (p->out_stride_b % 4 == 0) && ((p->seq * p->seq) % 4 == 0);
     const int nt = (p->seq + 15) / 16;
     hipStream_t st = static_cast<hipStream_t>(stream);
     switch (p->dtype) {
-        case ATX_DTYPE_BF16: return dispatch_kq<__bf16>(nt, p->batch, st, a);
-        case ATX_DTYPE_FP16: return dispatch_kq<_Float16>(nt, p->batch, st, a);
-        default: return dispatch_kq<float>(nt, p->batch, st, a);
+        case ATX_DTYPE_BF16: return dispatch_kq<__bf16>(nt, st, a);
+        case ATX_DTYPE_FP16: return dispatch_kq<_Float16>(nt, st, a);
+        default: return dispatch_kq<float>(nt, st, a);
     }
 }
