@@ -43,26 +43,36 @@ struct AttnArgs {
     int64_t osb, oss, osh;
     const uint8_t* kpad;
     int64_t kpsb;
+    int kpad_w4;  // padding rows 4-byte aligned
     int H, group, Sq, Skv, nkt;
     float c2;  // scale * log2(e)
     int causal;
+    int xcd_remap;  // H % 8 == 0: rotate heads by batch so each XCD sees all heads
 };
 
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 
 // Per-lane bitmask of usable keys (bit 4*kt + i <-> key 16*kt + 4*g + i):
-// inside the key range and not padded out.
+// inside the key range and not padded out.  The four padding bytes of one
+// (tile, lane group) are contiguous: one 4-byte load when the rows are 4-byte
+// aligned, else byte loads.
 __device__ inline uint64_t key_valid_bits(const AttnArgs& a, int b, int g, int nkt) {
     uint64_t bits = 0;
     const uint8_t* row = a.kpad ? a.kpad + (int64_t)b * a.kpsb : nullptr;
     for (int kt = 0; kt < nkt; ++kt) {
-        for (int i = 0; i < 4; ++i) {
-            int key = kt * 16 + 4 * g + i;
-            bool ok = key < a.Skv;
-            if (ok && row) ok = row[key] == 0;
-            if (ok) bits |= (uint64_t)1 << (4 * kt + i);
+        const int key0 = kt * 16 + 4 * g;
+        uint32_t pad = 0;  // byte i nonzero: key key0 + i is padded out
+        if (row && key0 < a.Skv) {
+            if (a.kpad_w4 && key0 + 4 <= a.Skv) {
+                pad = *reinterpret_cast<const uint32_t*>(row + key0);
+            } else {
+                for (int i = 0; i < 4; ++i)
+                    if (key0 + i < a.Skv) pad |= (uint32_t)row[key0 + i] << (8 * i);
+            }
         }
+        for (int i = 0; i < 4; ++i)
+            if (key0 + i < a.Skv && ((pad >> (8 * i)) & 0xff) == 0) bits |= (uint64_t)1 << (4 * kt + i);
     }
     return bits;
 }
@@ -97,24 +107,24 @@ constexpr int kOcc16[4][8][8] = {
         {5, 5, 4, 4, 4, 4, 4, 4},
     },
     {
+        {8, 8, 8, 8, 8, 6, 5, 4},
         {8, 8, 8, 8, 7, 6, 5, 4},
         {8, 8, 8, 8, 7, 6, 5, 4},
-        {8, 8, 8, 8, 6, 5, 5, 4},
-        {8, 7, 5, 4, 4, 3, 3, 2},
-        {8, 8, 7, 6, 5, 5, 4, 4},
-        {7, 7, 6, 6, 5, 4, 4, 4},
-        {6, 6, 5, 5, 5, 4, 4, 4},
-        {4, 4, 4, 4, 3, 3, 2, 2},
+        {8, 8, 7, 7, 6, 5, 5, 4},
+        {8, 8, 7, 7, 6, 5, 5, 4},
+        {7, 7, 7, 6, 5, 5, 4, 4},
+        {6, 6, 6, 5, 5, 5, 4, 4},
+        {5, 4, 4, 4, 4, 4, 4, 4},
     },
     {
-        {8, 8, 8, 8, 7, 5, 5, 4},
+        {8, 8, 8, 8, 7, 6, 5, 4},
         {8, 8, 8, 8, 6, 5, 5, 4},
-        {8, 8, 8, 7, 6, 5, 4, 4},
-        {7, 6, 5, 4, 4, 3, 3, 2},
-        {8, 7, 6, 6, 5, 4, 4, 4},
-        {8, 7, 6, 6, 5, 4, 4, 4},
-        {7, 6, 5, 5, 5, 4, 4, 4},
-        {4, 3, 4, 3, 3, 3, 2, 2},
+        {8, 8, 8, 7, 5, 5, 4, 4},
+        {8, 8, 8, 6, 5, 5, 4, 4},
+        {8, 8, 7, 5, 5, 5, 4, 4},
+        {8, 7, 6, 6, 5, 5, 4, 4},
+        {7, 5, 5, 5, 5, 4, 4, 4},
+        {5, 5, 4, 4, 4, 4, 4, 3},
     },
 };
 constexpr int kOcc32[8][8] = {
@@ -179,8 +189,17 @@ void attn_fwd_16bit(AttnArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int m = lane & 15, g = lane >> 4;
+    // Workgroups are dispatched round-robin over the 8 XCDs, so with H a
+    // multiple of 8 workgroup b*H + h would always land on XCD h % 8 (one
+    // head slice per XCD: measured 10-15 % slower).  Rotating the head by the
+    // batch index gives every XCD every head.
     const int bh = blockIdx.x;
-    const int b = bh / a.H, h = bh - b * a.H;
+    const int b = bh / a.H;
+    int h = bh - b * a.H;
+    if (a.xcd_remap) {
+        h += b & 7;
+        if (h >= a.H) h -= a.H;
+    }
     const int hk = h / a.group;
     const int qss = (int)a.qss, kss = (int)a.kss, vss = (int)a.vss, oss = (int)a.oss;
 
@@ -301,15 +320,34 @@ void attn_fwd_16bit(AttnArgs a) {
 
         // ---- mask -----------------------------------------------------------
         if constexpr (MASKED) {
+            // Usable-key bits of this query row: padding / range bits, and
+            // under causal masking keys 16kt + 4g + i <= qrow, i.e. the low
+            // clamp(qrow - 16kt - 4g + 1, 0, 4) bits of nibble kt.  Each score
+            // is then kept or replaced by -inf with a bitwise select on its
+            // sign-extended bit (no per-element compare masks).
+            uint64_t ok = kbits;
+            if (a.causal) {
+                uint64_t cb = 0;
 #pragma unroll
-            for (int kt = 0; kt < NKT; ++kt)
+                for (int kt = 0; kt < NKT; ++kt) {
+                    const int n = min(max((int)qrow - (kt * 16 + 4 * g) + 1, 0), 4);
+                    cb |= (uint64_t)((1u << n) - 1u) << (4 * kt);
+                }
+                ok &= cb;
+            }
+            const uint32_t ok_lo = (uint32_t)ok, ok_hi = (uint32_t)(ok >> 32);
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt) {
+                u32x4 bits = __builtin_bit_cast(u32x4, s[kt]);  // whole-vector casts only
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int key = kt * 16 + 4 * g + i;
-                    bool ok = (kbits >> (4 * kt + i)) & 1;
-                    if (a.causal) ok = ok && key <= qrow;
-                    s[kt][i] = ok ? s[kt][i] : kNegInf;
+                    const int pos = 4 * kt + i;
+                    const uint32_t word = pos < 32 ? ok_lo : ok_hi;
+                    const uint32_t keep = (uint32_t)((int32_t)(word << (31 - (pos & 31))) >> 31);
+                    bits[i] = (bits[i] & keep) | (0xff800000u & ~keep);
                 }
+                s[kt] = __builtin_bit_cast(f32x4, bits);
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) s[NKT - 1][i] += kbias[i];
@@ -719,6 +757,7 @@ extern "C" int atx_attn_fwd(const AtxAttnParams* p, void* stream) {
     a.osb = p->o_stride_b; a.oss = oss; a.osh = p->o_stride_h;
     a.kpad = p->key_pad;
     a.kpsb = p->key_pad_stride_b;
+    a.kpad_w4 = p->key_pad && ((uintptr_t)p->key_pad % 4 == 0) && (p->key_pad_stride_b % 4 == 0);
     a.H = p->num_heads;
     a.group = p->num_heads / p->num_kv_heads;
     a.Sq = p->seq_q;
@@ -726,6 +765,7 @@ extern "C" int atx_attn_fwd(const AtxAttnParams* p, void* stream) {
     a.nkt = (p->seq_kv + 15) / 16;
     a.c2 = p->scale * kLog2e;
     a.causal = p->causal != 0;
+    a.xcd_remap = p->num_heads % 8 == 0;
     const int nkc = (p->seq_kv + 31) / 32;
     hipStream_t st = static_cast<hipStream_t>(stream);
     switch (p->dtype) {

@@ -190,22 +190,23 @@ def time_kq(torch, ops, batch, dev, steps, warmup):
 
 
 def _mean_launch_ms(torch, fn, steps, warmup):
-    """Mean duration of ``fn()`` (one kernel launch) over ``steps`` calls,
-    from events recorded on the current stream around each call.  A GPU-side
-    spin queued first lets the host enqueue every call before the GPU reaches
-    them, so host launch overhead of short kernels does not enter the times."""
+    """Mean time per call of ``fn()`` (one kernel launch) over ``steps``
+    back-to-back calls, from one event pair around them.  An untimed burst
+    queued right before keeps the GPU busy (and at its working clocks) while
+    the host enqueues the timed calls, so host launch overhead of short
+    kernels does not enter the time."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    if hasattr(torch.cuda, "_sleep"):
-        torch.cuda._sleep(20_000_000)  # ~10 ms of clock cycles
-    for i in range(steps):
-        ev[i].record()
+    for _ in range(max(warmup, 20)):
         fn()
-    ev[steps].record()
+    a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn()
+    z.record()
     torch.cuda.synchronize()
-    return sum(ev[i].elapsed_time(ev[i + 1]) for i in range(steps)) / steps
+    return a.elapsed_time(z) / steps
 
 
 def _leg(what, ms, nbytes, samples):
