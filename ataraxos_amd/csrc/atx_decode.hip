@@ -8,10 +8,14 @@
 //
 // One wave per (batch, head).  A key row is split over LPK lanes (one 16-byte
 // chunk each), so a wave covers 64/LPK keys per step with fully coalesced
-// 16-byte loads.  Each lane keeps an online softmax (running max, running sum,
-// accumulator for its chunk of V) over the keys of its lane slot; the slots
-// are merged with cross-lane exchanges at the end.  The work is pure
-// streaming (about 1 FLOP per byte), so it is bound by HBM bandwidth.
+// 16-byte loads.  Keys are taken in blocks of U steps whose loads are all in
+// flight together; each lane keeps a softmax (running max, running sum,
+// accumulator for its chunk of V) over the keys of its lane slot, rescaled
+// once per block; the slots are merged with cross-lane exchanges at the end.
+// The work is pure streaming (about 1 FLOP per byte), so it is bound by HBM
+// bandwidth and by how many loads are in flight.
+#include <algorithm>
+
 #include "atx_common.hpp"
 
 namespace atx {
@@ -31,6 +35,7 @@ struct DecArgs {
     const int32_t* lens;
     int B, H, group, len, cap;
     float c2;
+    uint32_t q_bytes, o_bytes, kc_bytes, vc_bytes, kn_bytes, vn_bytes;  // extents of this launch
 };
 
 namespace {
@@ -44,23 +49,44 @@ constexpr int pow2ceil(int x) {
     return p;
 }
 
+// Chunk operations: a 16-byte chunk of a row, the dot product of a q chunk
+// and a k chunk (fp32 accumulate), and the conversion of a v chunk to fp32.
 template <typename T>
-struct Elem;
+struct Chunk;
 template <>
-struct Elem<float> {
+struct Chunk<float> {
     static constexpr int N = 4;
+    __device__ static inline float dot(u32x4 q, u32x4 k) {
+        const f32x4 a = as_f32x4(q), b = as_f32x4(k);
+        return __builtin_fmaf(a[3], b[3], __builtin_fmaf(a[2], b[2], __builtin_fmaf(a[1], b[1], a[0] * b[0])));
+    }
     __device__ static inline void unpack(u32x4 v, float (&f)[4]) {
+        const f32x4 x = as_f32x4(v);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) f[i] = as_f32x4(v)[i];
+        for (int i = 0; i < 4; ++i) f[i] = x[i];
     }
     __device__ static inline u32x4 pack(const float (&f)[4]) {
-        return u32x4{__builtin_bit_cast(uint32_t, f[0]), __builtin_bit_cast(uint32_t, f[1]),
-                     __builtin_bit_cast(uint32_t, f[2]), __builtin_bit_cast(uint32_t, f[3])};
+        return __builtin_bit_cast(u32x4, f32x4{f[0], f[1], f[2], f[3]});
     }
 };
 template <typename T16>
-struct Elem16 {
+struct Chunk16 {
     static constexpr int N = 8;
+    typedef T16 v8 __attribute__((ext_vector_type(8)));
+    typedef T16 v2 __attribute__((ext_vector_type(2)));
+    // Products of two 16-bit floats are exact in fp32; v_dot2 adds two of
+    // them to an fp32 accumulator.  (Sub-vectors are taken with shuffles of
+    // the whole vector, never by casting single elements.)
+    __device__ static inline float dot(u32x4 q, u32x4 k) {
+        const v8 a = __builtin_bit_cast(v8, q), b = __builtin_bit_cast(v8, k);
+        float r = 0.f;
+        r = dot2(__builtin_shufflevector(a, a, 0, 1), __builtin_shufflevector(b, b, 0, 1), r);
+        r = dot2(__builtin_shufflevector(a, a, 2, 3), __builtin_shufflevector(b, b, 2, 3), r);
+        r = dot2(__builtin_shufflevector(a, a, 4, 5), __builtin_shufflevector(b, b, 4, 5), r);
+        r = dot2(__builtin_shufflevector(a, a, 6, 7), __builtin_shufflevector(b, b, 6, 7), r);
+        return r;
+    }
+    __device__ static inline float dot2(v2 x, v2 y, float c);
     __device__ static inline void unpack(u32x4 v, float (&f)[8]) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -74,44 +100,77 @@ struct Elem16 {
     }
 };
 template <>
-struct Elem<__bf16> : Elem16<__bf16> {};
+__device__ inline float Chunk16<__bf16>::dot2(v2 x, v2 y, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(x, y, c, false);
+}
 template <>
-struct Elem<_Float16> : Elem16<_Float16> {};
+__device__ inline float Chunk16<_Float16>::dot2(v2 x, v2 y, float c) {
+    return __builtin_amdgcn_fdot2(x, y, c, false);
+}
+template <>
+struct Chunk<__bf16> : Chunk16<__bf16> {};
+template <>
+struct Chunk<_Float16> : Chunk16<_Float16> {};
 
 }  // namespace
 
+// Waves needed for P (batch, head) pairs at head_dim D.
+template <typename T>
+constexpr int dec_slots_per_wave(int D) {
+    return 64 / pow2ceil(D / Chunk<T>::N);
+}
+
+#ifndef ATX_DEC_KEYS
+#define ATX_DEC_KEYS 2
+#endif
+#ifndef ATX_DEC_WAVES
+#define ATX_DEC_WAVES 8
+#endif
+
 template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void attn_decode(DecArgs a) {
-    using E = Elem<T>;
-    constexpr int EPC = E::N;             // elements per 16-byte chunk
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(ATX_DEC_WAVES, 8)))
+void attn_decode(DecArgs a) {
+    using C = Chunk<T>;
+    constexpr int EPC = C::N;             // elements per 16-byte chunk
     constexpr int CH = D / EPC;           // chunks per row
-    constexpr int LPK = pow2ceil(CH);     // lanes per key
-    constexpr int KPI = 64 / LPK;         // keys per wave step
-    constexpr int U = KPI >= 8 ? 2 : 4;   // steps whose loads are issued together
+    constexpr int LPK = pow2ceil(CH);     // lanes per slot (one row per step)
+    constexpr int SPW = 64 / LPK;         // slots = (batch, head) pairs per wave
+    constexpr int U = ATX_DEC_KEYS;       // keys per block: all their loads in flight together
 
     const int lane = threadIdx.x & 63;
-    const int wid = blockIdx.x * kWaves + (threadIdx.x >> 6);
-    if (wid >= a.B * a.H) return;
-    const int b = wid / a.H, h = wid - (wid / a.H) * a.H;
-    const int hk = h / a.group;
     const int slot = lane / LPK, dc = lane % LPK;
-    const bool active = dc < CH;
+    const int pair = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * SPW + slot;
+    const bool valid = pair < a.B * a.H;
+    const bool active = valid && dc < CH;
+    const int pr = valid ? pair : 0;
+    const int b = pr / a.H, h = pr - (pr / a.H) * a.H;
+    const int hk = h / a.group;
 
-    int n = a.lens ? a.lens[b] : a.len;
+    int n = valid ? (a.lens ? a.lens[b] : a.len) : 0;
     n = n < a.cap ? n : a.cap;
-
-    const T* kb = static_cast<const T*>(a.kc) + b * a.ksb + hk * a.ksh;
-    const T* vb = static_cast<const T*>(a.vc) + b * a.vsb + hk * a.vsh;
-    const T* knew = a.kn ? static_cast<const T*>(a.kn) + b * a.knb + hk * a.knh : nullptr;
-    const T* vnew = a.vn ? static_cast<const T*>(a.vn) + b * a.vnb + hk * a.vnh : nullptr;
-
-    float qf[EPC];
-    {
-        const T* qrow = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
-        u32x4 qv = active ? ld16(qrow + dc * EPC) : u32x4{0, 0, 0, 0};
-        E::unpack(qv, qf);
+    int nmax = n;  // the wave's trip count
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) qf[e] *= a.c2;  // scores come out in log2 units
+    for (int off = LPK; off < 64; off <<= 1) nmax = max(nmax, __builtin_bit_cast(int, shfl_xor(__builtin_bit_cast(float, nmax), off)));
+    nmax = __builtin_amdgcn_readfirstlane(nmax);
+
+    // One buffer descriptor per tensor (uniform), 32-bit per-lane byte
+    // offsets (the host keeps every extent of one launch below 4 GiB).  A
+    // masked-out access gets an offset past the extent: loads return zero and
+    // stores are dropped by the range check, with no branches.
+    constexpr uint32_t es = sizeof(T);
+    constexpr uint32_t kOut = 0xfffffff0u;
+    const rsrc_t rk = make_rsrc(a.kc, a.kc_bytes), rv = make_rsrc(a.vc, a.vc_bytes);
+    const uint32_t chunk = (uint32_t)dc * 16;
+    const uint32_t koff = (uint32_t)(b * a.ksb + hk * a.ksh) * es + chunk;
+    const uint32_t voff = (uint32_t)(b * a.vsb + hk * a.vsh) * es + chunk;
+    const uint32_t kstep = (uint32_t)a.kss * es, vstep = (uint32_t)a.vss * es;
+    const bool has_new = a.kn != nullptr;
+    const u32x4 qv = buf_ld16(make_rsrc(a.q, a.q_bytes), active ? (uint32_t)(b * a.qsb + h * a.qsh) * es + chunk : kOut);
+    // the newest row, when given, comes from k_new / v_new
+    u32x4 knv = u32x4{0, 0, 0, 0}, vnv = u32x4{0, 0, 0, 0};
+    if (has_new) {
+        knv = buf_ld16(make_rsrc(a.kn, a.kn_bytes), active ? (uint32_t)(b * a.knb + hk * a.knh) * es + chunk : kOut);
+        vnv = buf_ld16(make_rsrc(a.vn, a.vn_bytes), active ? (uint32_t)(b * a.vnb + hk * a.vnh) * es + chunk : kOut);
     }
 
     const float kNegInf = -__builtin_inff();
@@ -120,100 +179,91 @@ __global__ __launch_bounds__(kThreads) void attn_decode(DecArgs a) {
 #pragma unroll
     for (int e = 0; e < EPC; ++e) acc[e] = 0.f;
 
-    for (int base = 0; base < n; base += U * KPI) {
+    for (int base = 0; base < nmax; base += U) {
         u32x4 kv[U], vv[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int key = base + u * KPI + slot;
-            const bool ok = active && key < n;
-            const bool fresh = knew && key == n - 1;
-            const T* kp = fresh ? knew : kb + key * a.kss;
-            const T* vp = fresh ? vnew : vb + key * a.vss;
-            kv[u] = ok ? ld16(kp + dc * EPC) : u32x4{0, 0, 0, 0};
-            vv[u] = ok ? ld16(vp + dc * EPC) : u32x4{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int key = base + u * KPI + slot;
-            float kf[EPC];
-            E::unpack(kv[u], kf);
-            float dot = 0.f;
-#pragma unroll
-            for (int e = 0; e < EPC; ++e) dot = __builtin_fmaf(qf[e], kf[e], dot);
-#pragma unroll
-            for (int off = 1; off < LPK; off <<= 1) dot += shfl_xor(dot, off);
-            if (key < n) {
-                const float mnew = fmaxf(mrun, dot);
-                const float alpha = fast_exp2(mrun - mnew);  // 0 while mrun = -inf
-                const float p = fast_exp2(dot - mnew);
-                float vf[EPC];
-                E::unpack(vv[u], vf);
-                lrun = lrun * alpha + p;
-#pragma unroll
-                for (int e = 0; e < EPC; ++e) acc[e] = __builtin_fmaf(p, vf[e], acc[e] * alpha);
-                mrun = mnew;
+            const int key = base + u;
+            const bool fresh = has_new && key == n - 1;
+            const bool ok = active && key < n && !fresh;
+            kv[u] = buf_ld16(rk, ok ? koff + (uint32_t)key * kstep : kOut);
+            vv[u] = buf_ld16(rv, ok ? voff + (uint32_t)key * vstep : kOut);
+            if (fresh) {
+                kv[u] = knv;
+                vv[u] = vnv;
             }
         }
-    }
-
-    // Merge the KPI key slots.
+        // scores of the block in log2 units (keys past n: -inf), one rescale
+        float sc[U];
+        float mblk = kNegInf;
 #pragma unroll
-    for (int off = LPK; off < 64; off <<= 1) {
-        const float mo = shfl_xor(mrun, off);
-        const float lo = shfl_xor(lrun, off);
-        const float mnew = fmaxf(mrun, mo);
-        const bool empty = (mnew == kNegInf);
-        const float a1 = empty ? 0.f : fast_exp2(mrun - mnew);
-        const float a2 = empty ? 0.f : fast_exp2(mo - mnew);
-        lrun = lrun * a1 + lo * a2;
+        for (int u = 0; u < U; ++u) {
+            float d = C::dot(qv, kv[u]);
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) {
-            const float ao = shfl_xor(acc[e], off);
-            acc[e] = acc[e] * a1 + ao * a2;
+            for (int off = 1; off < LPK; off <<= 1) d += shfl_xor(d, off);
+            sc[u] = base + u < n ? d * a.c2 : kNegInf;
+            mblk = fmaxf(mblk, sc[u]);
+        }
+        const float mnew = fmaxf(mrun, mblk);
+        const float ms = mnew == kNegInf ? 0.f : mnew;  // no key yet: stays empty
+        const float alpha = fast_exp2(mrun - ms);
+        lrun *= alpha;
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) acc[e] *= alpha;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float p = fast_exp2(sc[u] - ms);
+            float vf[EPC];
+            C::unpack(vv[u], vf);
+            lrun += p;
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) acc[e] = __builtin_fmaf(p, vf[e], acc[e]);
         }
         mrun = mnew;
     }
 
-    if (slot == 0 && active) {
+    if (active) {
         // n < 1 leaves lrun = 0 and the result NaN, as a softmax over no keys.
         const float inv = 1.0f / lrun;
         float r[EPC];
 #pragma unroll
         for (int e = 0; e < EPC; ++e) r[e] = acc[e] * inv;
-        T* orow = static_cast<T*>(a.o) + b * a.osb + h * a.osh;
-        st16(orow + dc * EPC, E::pack(r));
+        buf_st16(make_rsrc(a.o, a.o_bytes), (uint32_t)(b * a.osb + h * a.osh) * es + chunk, C::pack(r));
         // The first query head of each KV group appends the new row.
-        if (knew && n >= 1 && h % a.group == 0) {
-            st16(static_cast<T*>(a.kc) + b * a.ksb + hk * a.ksh + (n - 1) * a.kss + dc * EPC, ld16(knew + dc * EPC));
-            st16(static_cast<T*>(a.vc) + b * a.vsb + hk * a.vsh + (n - 1) * a.vss + dc * EPC, ld16(vnew + dc * EPC));
+        if (has_new && n >= 1 && h % a.group == 0) {
+            buf_st16(rk, koff + (uint32_t)(n - 1) * kstep, knv);
+            buf_st16(rv, voff + (uint32_t)(n - 1) * vstep, vnv);
         }
     }
 }
 
 namespace {
 
-template <typename T>
-int dispatch_decode(int D, int grid, hipStream_t st, const DecArgs& a) {
-    switch (D) {
-#define ATX_DEC_CASE(N)                                                                  \
-    case N:                                                                              \
-        hipLaunchKernelGGL((attn_decode<T, N>), dim3(grid), dim3(kThreads), 0, st, a); \
-        break;
-        ATX_DEC_CASE(8)
-        ATX_DEC_CASE(16)
-        ATX_DEC_CASE(24)
-        ATX_DEC_CASE(32)
-        ATX_DEC_CASE(48)
-        ATX_DEC_CASE(64)
-        ATX_DEC_CASE(96)
-        ATX_DEC_CASE(128)
-        ATX_DEC_CASE(256)
-#undef ATX_DEC_CASE
-        default:
-            ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_decode_fwd: head_dim %d not supported", D);
-    }
+template <typename T, int D>
+int launch_decode(hipStream_t st, const DecArgs& a) {
+    constexpr int spw = dec_slots_per_wave<T>(D);
+    const int64_t waves = ((int64_t)a.B * a.H + spw - 1) / spw;
+    const int64_t grid = (waves + kWaves - 1) / kWaves;
+    if (grid > 0x7fffffff) ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_decode_fwd: batch*heads too large");
+    hipLaunchKernelGGL((attn_decode<T, D>), dim3((unsigned)grid), dim3(kThreads), 0, st, a);
     ATX_CHECK_LAUNCH("atx_attn_decode_fwd launch");
     return ATX_OK;
+}
+
+template <typename T>
+int dispatch_decode(int D, hipStream_t st, const DecArgs& a) {
+    switch (D) {
+        case 8: return launch_decode<T, 8>(st, a);
+        case 16: return launch_decode<T, 16>(st, a);
+        case 24: return launch_decode<T, 24>(st, a);
+        case 32: return launch_decode<T, 32>(st, a);
+        case 48: return launch_decode<T, 48>(st, a);
+        case 64: return launch_decode<T, 64>(st, a);
+        case 96: return launch_decode<T, 96>(st, a);
+        case 128: return launch_decode<T, 128>(st, a);
+        case 256: return launch_decode<T, 256>(st, a);
+        default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_decode_fwd: head_dim %d not supported", D);
+    }
 }
 
 }  // namespace
@@ -278,11 +328,54 @@ extern "C" int atx_attn_decode_fwd(const AtxDecodeParams* p, void* stream) {
     a.len = p->kv_len;
     a.cap = p->kv_capacity;
     a.c2 = p->scale * kLog2e;
-    const int grid = (int)((waves + kWaves - 1) / kWaves);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    switch (p->dtype) {
-        case ATX_DTYPE_BF16: return dispatch_decode<__bf16>(p->head_dim, grid, st, a);
-        case ATX_DTYPE_FP16: return dispatch_decode<_Float16>(p->head_dim, grid, st, a);
-        default: return dispatch_decode<float>(p->head_dim, grid, st, a);
+    // The kernel addresses each tensor with 32-bit byte offsets: launch over
+    // batch chunks whose every tensor extent stays below 4 GiB.
+    const int64_t D = p->head_dim, Hq = p->num_heads, Hk = p->num_kv_heads, T = p->kv_capacity;
+    struct Extent {
+        int64_t sb, rest;  // bytes per batch step; bytes of one batch element's slice
+    };
+    const Extent ext[] = {
+        {p->q_stride_b * es, ((Hq - 1) * p->q_stride_h + D) * es},
+        {p->o_stride_b * es, ((Hq - 1) * p->o_stride_h + D) * es},
+        {p->k_stride_b * es, ((Hk - 1) * p->k_stride_h + (T - 1) * p->k_stride_s + D) * es},
+        {p->v_stride_b * es, ((Hk - 1) * p->v_stride_h + (T - 1) * p->v_stride_s + D) * es},
+        {p->k_new ? p->k_new_stride_b * es : 0, p->k_new ? ((Hk - 1) * p->k_new_stride_h + D) * es : 0},
+        {p->v_new ? p->v_new_stride_b * es : 0, p->v_new ? ((Hk - 1) * p->v_new_stride_h + D) * es : 0},
+    };
+    const int64_t lim = 0xffffff00LL;  // below the out-of-range offset the kernel uses for masked lanes
+    int64_t nb = p->batch;
+    for (const Extent& e : ext) {
+        if (e.sb < 0 || e.rest < 0 || e.rest > lim)
+            ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_decode_fwd: strides must be >= 0 and one batch element < 4 GiB");
+        if (e.sb > 0) nb = std::min<int64_t>(nb, 1 + (lim - e.rest) / e.sb);
     }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    for (int64_t b0 = 0; b0 < p->batch; b0 += nb) {
+        DecArgs c = a;
+        c.B = (int)std::min<int64_t>(nb, p->batch - b0);
+        c.q = static_cast<const char*>(p->q) + b0 * ext[0].sb;
+        c.o = static_cast<char*>(p->o) + b0 * ext[1].sb;
+        c.kc = static_cast<char*>(p->k_cache) + b0 * ext[2].sb;
+        c.vc = static_cast<char*>(p->v_cache) + b0 * ext[3].sb;
+        if (p->k_new) {
+            c.kn = static_cast<const char*>(p->k_new) + b0 * ext[4].sb;
+            c.vn = static_cast<const char*>(p->v_new) + b0 * ext[5].sb;
+        }
+        if (p->kv_lens) c.lens = p->kv_lens + b0;
+        auto bytes = [&](const Extent& e) { return (uint32_t)((c.B - 1) * e.sb + e.rest); };
+        c.q_bytes = bytes(ext[0]);
+        c.o_bytes = bytes(ext[1]);
+        c.kc_bytes = bytes(ext[2]);
+        c.vc_bytes = bytes(ext[3]);
+        c.kn_bytes = p->k_new ? bytes(ext[4]) : 0;
+        c.vn_bytes = p->v_new ? bytes(ext[5]) : 0;
+        int rc;
+        switch (p->dtype) {
+            case ATX_DTYPE_BF16: rc = dispatch_decode<__bf16>(p->head_dim, st, c); break;
+            case ATX_DTYPE_FP16: rc = dispatch_decode<_Float16>(p->head_dim, st, c); break;
+            default: rc = dispatch_decode<float>(p->head_dim, st, c); break;
+        }
+        if (rc != ATX_OK) return rc;
+    }
+    return ATX_OK;
 }
