@@ -4,14 +4,18 @@
   its GPU path is one fused HIP kernel (``libataraxos_attn.so``).
 * :class:`KeyQueryPolicyHead` — drop-in for the Move network's policy head,
   with the logits, legal-move mask and softmax fused on the GPU.
-* :class:`KVCache` / :func:`ops.attention_decode` — incremental causal decode.
+* :class:`KVCache` / :func:`ops.attention_decode` — incremental causal decode;
+  :class:`SetupDecoder` runs a Setup network token by token over it.
+* :func:`use_hip_attention` / :class:`KernelMultiheadAttention` — the Belief
+  network's ``nn.TransformerDecoder`` attention through the same kernel.
 
 Importing the package does not load the library or touch the GPU.
 """
 
 from . import ops
 from .attention import MultiHeadAttention, math_attention
-from .decode import KVCache
+from .decode import KVCache, SetupDecoder
+from .decoder import KernelMultiheadAttention, use_hip_attention
 from .policy import KeyQueryPolicyHead, masked_policy_logits, masked_policy_softmax
 
 __all__ = [
@@ -22,4 +26,7 @@ __all__ = [
     "masked_policy_logits",
     "masked_policy_softmax",
     "KVCache",
+    "SetupDecoder",
+    "KernelMultiheadAttention",
+    "use_hip_attention",
 ]

@@ -14,7 +14,7 @@ import torch
 
 from . import ops
 
-__all__ = ["KVCache"]
+__all__ = ["KVCache", "SetupDecoder"]
 
 
 class KVCache:
@@ -68,3 +68,56 @@ class KVCache:
 
     def advance(self) -> None:
         self.length += 1
+
+
+class SetupDecoder:
+    """Token-by-token evaluation of a Setup network over per-layer KV caches.
+
+    ``net`` is the reference ``SetupNetwork`` (``stratego/networks/setup_net.py:80-123``)
+    or any module with its structure: ``token_emb``, ``pos_emb.embed``,
+    ``blocks.blocks[i]`` pre-LN blocks with ``ln1`` / ``attn`` (q/k/v/out
+    projections) / ``ln2`` / ``ff`` (``stratego/networks/transformer.py:117-145``),
+    and ``value_head`` / ``entropy_head`` / ``policy_head``.  The network is
+    causal, so the output at position t depends only on tokens 0..t: one
+    :meth:`step` per placed piece gives what the reference gets by re-running
+    the network over the whole prefix (``selfplay.py:139-146,181``), with one
+    query row per layer instead of t.
+
+    :meth:`step` returns ``(value_logits [B, 3], entropy [B],
+    policy_logits [B, num_types])``: the value and entropy heads read position
+    0 (``transformer.py:193-250``), the policy the newest position
+    (``selfplay.py:182``).
+    """
+
+    def __init__(self, net: torch.nn.Module, batch: int, capacity: int = 40) -> None:
+        self.net = net
+        blocks = list(net.blocks.blocks)
+        attn = blocks[0].attn
+        p = next(net.parameters())
+        self.heads, self.kv_heads, self.head_dim = attn.num_heads, attn.num_kv_heads, attn.head_dim
+        self.cache = KVCache(len(blocks), batch, self.kv_heads, capacity, self.head_dim, dtype=p.dtype, device=p.device)
+        self.first: torch.Tensor | None = None  # position 0's output (value / entropy heads)
+
+    def reset(self) -> None:
+        self.cache.reset()
+        self.first = None
+
+    @torch.no_grad()
+    def step(self, tokens: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """Feed the newest token ``[B]`` (int) of every sequence."""
+        net, t = self.net, self.cache.length
+        x = net.token_emb(tokens) + net.pos_emb.embed[t]
+        b = x.shape[0]
+        for layer, blk in enumerate(net.blocks.blocks):
+            a = blk.attn
+            hn = blk.ln1(x)
+            q = a.q_proj(hn).view(b, self.heads, self.head_dim)
+            k = a.k_proj(hn).view(b, self.kv_heads, self.head_dim)
+            v = a.v_proj(hn).view(b, self.kv_heads, self.head_dim)
+            o = self.cache.step(layer, q, k, v)
+            x = x + a.out_proj(o.reshape(b, -1))
+            x = x + blk.ff(blk.ln2(x))
+        self.cache.advance()
+        if self.first is None:
+            self.first = x
+        return net.value_head(self.first), net.entropy_head(self.first), net.policy_head(x)

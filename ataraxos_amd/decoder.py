@@ -1,0 +1,101 @@
+"""The Belief network's decoder attention through the fused kernel.
+
+The reference's Belief decoder is ``nn.TransformerDecoder`` over
+``nn.TransformerDecoderLayer(batch_first=True, norm_first=True)``
+(``stratego/networks/belief_net.py:105-114``), called with a float causal
+``tgt_mask`` (``triu(full(-inf), 1)``, ``belief_net.py:167-170``) and a bool
+``memory_key_padding_mask = ~hidden_mask`` (``belief_net.py:159,172-177``).
+Inside, each layer calls ``self_attn`` and ``multihead_attn``, both
+``nn.MultiheadAttention`` with a packed ``in_proj_weight [3E, E]``,
+``in_proj_bias`` and a biased ``out_proj``.
+
+:class:`KernelMultiheadAttention` is ``nn.MultiheadAttention`` with the same
+parameters, ``state_dict`` keys and call signature, whose GPU forward runs
+the projections as ``F.linear`` and the attention as one HIP kernel launch
+(causal self-attention; cross-attention with key padding).
+:func:`use_hip_attention` converts every ``nn.MultiheadAttention`` inside a
+module in place, so an existing decoder (and its checkpoint) is used as is.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+
+__all__ = ["KernelMultiheadAttention", "use_hip_attention"]
+
+
+class KernelMultiheadAttention(nn.MultiheadAttention):
+    """``nn.MultiheadAttention`` whose GPU forward is the fused HIP kernel.
+
+    Covered on the GPU: ``need_weights=False`` (what ``TransformerDecoderLayer``
+    passes), no mask or the causal mask (``is_causal=True``, the hint
+    ``nn.TransformerDecoder`` derives from a ``triu(-inf, 1)`` mask), and a
+    bool ``key_padding_mask`` ``[B, S_kv]`` (True = ignore).  Anything else
+    raises on the GPU instead of silently taking another path.  On the CPU,
+    and in training with dropout > 0 (the kernel has no dropout), the forward
+    is ``nn.MultiheadAttention``'s own, as in the reference.
+    """
+
+    def forward(  # type: ignore[override]
+        self,
+        query: torch.Tensor,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        key_padding_mask: torch.Tensor | None = None,
+        need_weights: bool = True,
+        attn_mask: torch.Tensor | None = None,
+        average_attn_weights: bool = True,
+        is_causal: bool = False,
+    ) -> tuple[torch.Tensor, torch.Tensor | None]:
+        if not query.is_cuda or (self.training and self.dropout > 0.0):
+            return super().forward(
+                query, key, value, key_padding_mask=key_padding_mask, need_weights=need_weights,
+                attn_mask=attn_mask, average_attn_weights=average_attn_weights, is_causal=is_causal,
+            )
+        if need_weights:
+            raise NotImplementedError("KernelMultiheadAttention on the GPU returns no weights: pass need_weights=False")
+        if attn_mask is not None and not is_causal:
+            raise NotImplementedError(
+                "KernelMultiheadAttention on the GPU supports no attn_mask other than the causal one (is_causal=True)"
+            )
+        if key_padding_mask is not None and key_padding_mask.dtype != torch.bool:
+            raise NotImplementedError("KernelMultiheadAttention on the GPU takes a bool key_padding_mask")
+        if not self.batch_first:
+            query, key, value = (t.transpose(0, 1) for t in (query, key, value))
+        b, sq, e = query.shape
+        skv = key.shape[1]
+        h = self.num_heads
+        d = e // h
+        if self._qkv_same_embed_dim:
+            w_q, w_k, w_v = self.in_proj_weight.chunk(3)
+        else:
+            w_q, w_k, w_v = self.q_proj_weight, self.k_proj_weight, self.v_proj_weight
+        b_q = b_k = b_v = None
+        if self.in_proj_bias is not None:
+            b_q, b_k, b_v = self.in_proj_bias.chunk(3)
+        q = F.linear(query, w_q, b_q).view(b, sq, h, d)
+        k = F.linear(key, w_k, b_k).view(b, skv, h, d)
+        v = F.linear(value, w_v, b_v).view(b, skv, h, d)
+        o = ops.attention(q, k, v, causal=is_causal, key_padding_mask=key_padding_mask)
+        out = self.out_proj(o.reshape(b, sq, e))
+        if not self.batch_first:
+            out = out.transpose(0, 1)
+        return out, None
+
+
+def use_hip_attention(module: nn.Module) -> nn.Module:
+    """Convert every ``nn.MultiheadAttention`` inside ``module`` (itself
+    included) to :class:`KernelMultiheadAttention`, in place: parameters,
+    buffers and ``state_dict`` keys are unchanged.  Returns ``module``."""
+    for m in module.modules():
+        if type(m) is nn.MultiheadAttention:
+            if m.bias_k is not None or m.add_zero_attn:
+                raise NotImplementedError("use_hip_attention: add_bias_kv / add_zero_attn are not supported")
+            if (m.embed_dim // m.num_heads) % 16 != 0:
+                raise NotImplementedError(f"use_hip_attention: head_dim {m.embed_dim // m.num_heads} not supported")
+            m.__class__ = KernelMultiheadAttention
+    return module

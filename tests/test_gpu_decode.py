@@ -110,3 +110,31 @@ def test_decode_equals_causal_recompute_per_step(cuda):
     for t in (1, 2, 20, 40):
         step = ops.attention_decode(q[:, t - 1], kc, vc, t)
         np.testing.assert_allclose(step.cpu().numpy(), full[:, t - 1].cpu().numpy(), rtol=0, atol=2e-6)
+
+
+def test_cache_views_wider_than_4gib(cuda):
+    """Caches whose batch stride makes one launch's extent exceed 4 GiB: the
+    library splits the launch by batch (the kernel uses 32-bit offsets).  The
+    views cover 10 batch rows 2^28 elements apart (~4.5 GiB each)."""
+    _announce("decode over > 4 GiB cache views, with k_new/v_new")
+    b, h, t, d = 10, 2, 8, 64
+    sb = 1 << 28
+    q = randn((b, h, d), 71, torch.bfloat16)
+    kvals = randn((b, h, t, d), 72, torch.bfloat16)
+    vvals = randn((b, h, t, d), 73, torch.bfloat16)
+    kn = randn((b, h, d), 74, torch.bfloat16)
+    vn = randn((b, h, d), 75, torch.bfloat16)
+    caches = []
+    for vals in (kvals, vvals):
+        buf = torch.zeros(sb * (b - 1) + h * t * d, dtype=torch.bfloat16, device=cuda)
+        view = buf.as_strided((b, h, t, d), (sb, t * d, d, 1))
+        view.copy_(vals.to(cuda))
+        caches.append((buf, view))
+    (kbuf, kc), (vbuf, vc) = caches
+    out = ops.attention_decode(q.to(cuda), kc, vc, t, kn.to(cuda), vn.to(cuda))
+    torch.cuda.synchronize()
+    kref, vref = to_np64(kvals), to_np64(vvals)
+    kref[:, :, t - 1], vref[:, :, t - 1] = to_np64(kn), to_np64(vn)
+    assert_close(out, decode_step(to_np64(q), kref, vref), torch.bfloat16, "decode > 4 GiB")
+    assert torch.equal(kc[:, :, t - 1].cpu(), kn) and torch.equal(vc[:, :, t - 1].cpu(), vn)
+    del kbuf, vbuf, caches
