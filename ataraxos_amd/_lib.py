@@ -137,8 +137,31 @@ class AtxError(RuntimeError):
 
 
 # Exported symbols, as declared in include/ataraxos_attn.h.
+class AttnBwdParams(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", _i32),
+        ("dtype", _i32),
+        ("batch", _i32),
+        ("seq_q", _i32),
+        ("seq_kv", _i32),
+        ("num_heads", _i32),
+        ("num_kv_heads", _i32),
+        ("head_dim", _i32),
+    ] + [
+        (f"{name}{suffix}" if suffix == "" else f"{name.replace('d_o', 'do')}{suffix}", t)
+        for name in ("q", "k", "v", "o", "d_o", "dq", "dk", "dv")
+        for suffix, t in (("", _ptr), ("_stride_b", _i64), ("_stride_s", _i64), ("_stride_h", _i64))
+    ] + [
+        ("scale", _f32),
+        ("causal", _i32),
+        ("key_pad", _ptr),
+        ("key_pad_stride_b", _i64),
+    ]
+
+
 ENTRY_POINTS = {
     "atx_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnParams), _ptr]),
+    "atx_attn_bwd": (ctypes.c_int, [ctypes.POINTER(AttnBwdParams), _ptr]),
     "atx_kq_masked_softmax_fwd": (ctypes.c_int, [ctypes.POINTER(KqParams), _ptr]),
     "atx_attn_decode_fwd": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr]),
     "atx_last_error": (ctypes.c_char_p, []),

@@ -1,0 +1,481 @@
+// Attention backward for gfx950 (bf16 / fp16): dQ, dK, dV of
+//   S = scale * Q K^T (masked), P = softmax(S), O = P V
+// given Q, K, V, O and dO -- the gradient the reference's training step
+// (stratego/training/move_trainer.py:140) takes through
+// stratego/networks/attention.py:281-316.  With delta_q = sum_d O[q,d] dO[q,d]:
+//   dP = dO V^T,  dS = P * (dP - delta),
+//   dQ = scale * dS K,  dK = scale * dS^T Q,  dV = P^T dO.
+//
+// One workgroup (4 waves) per (batch, head), everything for that pair
+// resident in LDS: K, V, Q and dO rows in one layout that serves both 16-byte
+// row reads and the transposing reads (ds_read_b64_tr_b16), plus the
+// per-query log-sum-exp and delta.
+//  * Phase 1, one wave per 16-query tile, in the forward's orientation
+//    (S^T = K Q^T: each lane owns one query): recompute the softmax and its
+//    log-sum-exp, then dP^T = V dO^T, dS^T, and dQ^T = K^T dS^T with dS^T
+//    fed from registers the way the forward feeds P^T.
+//  * Phase 2, one wave per 16-key tile (S = Q K^T: each lane owns one key):
+//    recompute P from the log-sum-exp, dP = dO V^T and dS, and accumulate
+//    dV^T = dO^T P and dK^T = Q^T dS over pairs of query tiles, with P and dS
+//    fed from registers.
+// Every output tile has one owner: no atomics, no cross-wave reductions, and
+// the result does not depend on timing.
+// Masked scores get dS = 0 exactly (the gradient of masked_fill); a query
+// that sees no key has P = NaN, so its dO reaches dV as NaN, as autograd
+// through the reference's math gives.
+#include "ataraxos_attn.h"
+#include "atx_common.hpp"
+
+namespace atx {
+
+struct BwdArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* o;
+    const void* dout;
+    void* dq;
+    void* dk;
+    void* dv;
+    int64_t qsb, qsh, ksb, ksh, vsb, vsh, osb, osh, dosb, dosh, dqsb, dqsh, dksb, dksh, dvsb, dvsh;
+    int qss, kss, vss, oss, doss, dqss, dkss, dvss;  // sequence strides (elements)
+    const uint8_t* kpad;
+    int64_t kpsb;
+    int H, Sq, Skv;
+    float c2, scale;  // c2 = scale * log2(e)
+    int causal;
+};
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+
+// Row layout shared by every staged matrix.  At D = 64 / 128 the 16-byte
+// chunk c of row r sits at c ^ ((r >> 1) & 7): the 16 rows of an MFMA operand
+// read and the 4 rows x 4 column groups of a transposing read both fall in
+// distinct bank groups.  Other D pad rows to an odd number of 16-byte units.
+template <int D>
+constexpr bool kSwz = (D == 64 || D == 128);
+template <int D>
+constexpr int row_bytes() {
+    return kSwz<D> ? D * 2 : D * 2 + 16;
+}
+// Row r, 16-byte chunk c.  The swizzle depends on r mod 16 only, so tile
+// offsets (multiples of 16 rows) add on.
+template <int D>
+__device__ inline int chunk_off(int r, int c) {
+    return r * row_bytes<D>() + (kSwz<D> ? (c ^ ((r >> 1) & 7)) : c) * 16;
+}
+// Row r, elements e .. e+3 (e a multiple of 4): one 8-byte unit.
+template <int D>
+__device__ inline int quad_off(int r, int e) {
+    return chunk_off<D>(r, e >> 3) + (e & 7) * 2;
+}
+
+// x where bit `bit` of `bits` is set, else +0 (a mask, not a compare: the
+// bit index is a compile-time constant after unrolling).
+__device__ inline float keep_bit(float x, uint64_t bits, int bit) {
+    const uint32_t w = bit < 32 ? (uint32_t)bits : (uint32_t)(bits >> 32);
+    const uint32_t m = (uint32_t)((int32_t)(w << (31 - (bit & 31))) >> 31);
+    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) & m);
+}
+
+}  // namespace
+
+// Bytes of LDS for one workgroup.
+inline size_t bwd_lds_bytes(int D, int rk, int rq) {
+    const int rs = (D == 64 || D == 128) ? D * 2 : D * 2 + 16;
+    return (size_t)(2 * rk + 2 * rq) * rs + (size_t)rq * 4 * (2 + D / 8);
+}
+
+// NKC = 32-key chunks (S_kv <= 32 * NKC).
+template <typename T, int D, int NKC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8)))
+void attn_bwd_16bit(BwdArgs a) {
+    using M = Mfma16<T>;
+    constexpr int CH = D / 8;          // 16-byte chunks per row
+    constexpr int NI = (D + 31) / 32;  // MFMAs per 16x16 score tile
+    constexpr int NDT = D / 16;        // head-dim output tiles
+    constexpr int QD = D / 4;          // contiguous outputs per lane
+    constexpr int NKT = 2 * NKC;       // key tiles
+    constexpr int RK = NKT * 16;       // K / V rows staged
+    constexpr int RS = row_bytes<D>();
+
+    const int nqt = (a.Sq + 15) >> 4;
+    const int nqp = (nqt + 1) >> 1;  // pairs of query tiles
+    const int RQ = nqp * 32;         // Q / dO rows staged
+
+    lds_t* const sk = lds_base();
+    lds_t* const sv = sk + RK * RS;
+    lds_t* const sq = sv + RK * RS;
+    lds_t* const sdo = sq + RQ * RS;
+    lds_t* const slse = sdo + RQ * RS;  // RQ floats: log-sum-exp in log2 units
+    lds_t* const sdelta = slse + RQ * 4;  // RQ floats
+    lds_t* const spart = sdelta + RQ * 4;  // RQ x CH floats: partial dots of delta
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int m = lane & 15, g = lane >> 4;
+    const int b = blockIdx.x / a.H, h = blockIdx.x - (blockIdx.x / a.H) * a.H;
+    const float kNegInf = -__builtin_inff();
+
+    // One descriptor per tensor slice, ending at its last row: rows past S
+    // read as zero, output rows past S are dropped.
+    auto slice = [&](const void* base, int64_t sb, int64_t sh, int ss, int rows) {
+        return make_rsrc(static_cast<const T*>(base) + b * sb + h * sh, (uint32_t)(((rows - 1) * ss + D) * 2));
+    };
+    const rsrc_t rq = slice(a.q, a.qsb, a.qsh, a.qss, a.Sq);
+    const rsrc_t rk = slice(a.k, a.ksb, a.ksh, a.kss, a.Skv);
+    const rsrc_t rv = slice(a.v, a.vsb, a.vsh, a.vss, a.Skv);
+    const rsrc_t ro = slice(a.o, a.osb, a.osh, a.oss, a.Sq);
+    const rsrc_t rdo = slice(a.dout, a.dosb, a.dosh, a.doss, a.Sq);
+    const rsrc_t rdq = slice(a.dq, a.dqsb, a.dqsh, a.dqss, a.Sq);
+    const rsrc_t rdk = slice(a.dk, a.dksb, a.dksh, a.dkss, a.Skv);
+    const rsrc_t rdv = slice(a.dv, a.dvsb, a.dvsh, a.dvss, a.Skv);
+
+    // ---- stage K, V (RK rows), Q, dO (RQ rows); partial dots O . dO --------
+    for (int idx = tid; idx < RK * CH; idx += kThreads) {
+        const int r = idx / CH, c = idx - (idx / CH) * CH;
+        lds_st16(sk + chunk_off<D>(r, c), buf_ld16(rk, (uint32_t)(r * a.kss + c * 8) * 2));
+        lds_st16(sv + chunk_off<D>(r, c), buf_ld16(rv, (uint32_t)(r * a.vss + c * 8) * 2));
+    }
+    for (int idx = tid; idx < RQ * CH; idx += kThreads) {
+        const int r = idx / CH, c = idx - (idx / CH) * CH;
+        const u32x4 qv = buf_ld16(rq, (uint32_t)(r * a.qss + c * 8) * 2);
+        const u32x4 dv = buf_ld16(rdo, (uint32_t)(r * a.doss + c * 8) * 2);
+        const u32x4 ov = buf_ld16(ro, (uint32_t)(r * a.oss + c * 8) * 2);
+        lds_st16(sq + chunk_off<D>(r, c), qv);
+        lds_st16(sdo + chunk_off<D>(r, c), dv);
+        float part = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            part = __builtin_fmaf(M::to_float((uint16_t)(ov[j] & 0xffffu)), M::to_float((uint16_t)(dv[j] & 0xffffu)), part);
+            part = __builtin_fmaf(M::to_float((uint16_t)(ov[j] >> 16)), M::to_float((uint16_t)(dv[j] >> 16)), part);
+        }
+        lds_st4(spart + idx * 4, __builtin_bit_cast(uint32_t, part));
+    }
+    __syncthreads();
+    // delta_q: each row's partials summed in a fixed order.  The log-sum-exp
+    // starts at 0 for every staged row; phase 1 overwrites the rows it covers.
+    for (int r = tid; r < RQ; r += kThreads) {
+        float d = 0.f;
+        for (int c = 0; c < CH; ++c) d += __builtin_bit_cast(float, lds_ld4(spart + (r * CH + c) * 4));
+        lds_st4(sdelta + r * 4, __builtin_bit_cast(uint32_t, d));
+        lds_st4(slse + r * 4, 0u);
+    }
+
+    // Usable keys of this lane in phase 1 (bit 4*kt + i <-> key 16*kt + 4g + i).
+    uint64_t kbits = 0;
+    const uint8_t* prow = a.kpad ? a.kpad + (int64_t)b * a.kpsb : nullptr;
+    for (int kt = 0; kt < NKT; ++kt)
+        for (int i = 0; i < 4; ++i) {
+            const int key = kt * 16 + 4 * g + i;
+            if (key < a.Skv && !(prow && prow[key])) kbits |= (uint64_t)1 << (4 * kt + i);
+        }
+    __syncthreads();
+
+    // Per-lane LDS offsets.  Operand reads of 16-row tiles: row m, chunks
+    // 4i + g.  Transposing reads: input lane a4 + 4t of a 16-lane group points
+    // at row 4g + t and elements a4*QD + 4dt .. +3, which hands lane m the
+    // four rows 4g .. 4g+3 of head-dim (m/4)*QD + 4dt + m%4.
+    int coff[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) coff[i] = chunk_off<D>(m, 4 * i + g);
+    int troff[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) troff[dt] = quad_off<D>(4 * g + (m >> 2), (m & 3) * QD + 4 * dt);
+    auto ld_op = [&](const lds_t* base, int i) {
+        u32x4 v = lds_ld16(base + coff[i]);
+        if (CH % 4 != 0 && 4 * i + g >= CH) v = u32x4{0, 0, 0, 0};
+        return v;
+    };
+    // Stores QD contiguous elements d = g*QD .. of row `row` from four-element
+    // groups x[dt] (d = g*QD + 4dt + i), scaled.
+    auto store_row = [&](rsrc_t r, int ss, int row, const f32x4 (&x)[NDT], float mul) {
+        const uint32_t base = (uint32_t)(row * ss + g * QD) * 2;
+        if constexpr (QD % 8 == 0) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt += 2)
+                buf_st16_cached(r, base + dt * 8,
+                                u32x4{M::pack2(x[dt][0] * mul, x[dt][1] * mul), M::pack2(x[dt][2] * mul, x[dt][3] * mul),
+                                      M::pack2(x[dt + 1][0] * mul, x[dt + 1][1] * mul),
+                                      M::pack2(x[dt + 1][2] * mul, x[dt + 1][3] * mul)});
+        } else {
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+                buf_st8_cached(r, base + dt * 8,
+                               u32x2{M::pack2(x[dt][0] * mul, x[dt][1] * mul), M::pack2(x[dt][2] * mul, x[dt][3] * mul)});
+        }
+    };
+
+    // ---- phase 1: one 16-query tile per wave pass --------------------------
+    for (int qt = wave; qt < nqt; qt += kWaves) {
+        const int qrow = qt * 16 + m;
+        const lds_t* const qbase = sq + qt * 16 * RS;
+        const lds_t* const dobase = sdo + qt * 16 * RS;
+        u32x4 qop[NI], doop[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            qop[i] = ld_op(qbase, i);
+            doop[i] = ld_op(dobase, i);
+        }
+        // usable keys of this query row
+        uint64_t ok = kbits;
+        if (a.causal) {
+            uint64_t cb = 0;
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt) {
+                const int n = min(max(qrow - (kt * 16 + 4 * g) + 1, 0), 4);
+                cb |= (uint64_t)((1u << n) - 1u) << (4 * kt);
+            }
+            ok &= cb;
+        }
+        // S^T = K Q^T, masked, in log2 units
+        f32x4 s[NKT];
+        float mx = kNegInf;
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < NI; ++i) acc = M::mma(ld_op(sk + kt * 16 * RS, i), qop[i], acc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc[i] = ((ok >> (4 * kt + i)) & 1) ? acc[i] * a.c2 : kNegInf;
+                mx = fmaxf(mx, acc[i]);
+            }
+            s[kt] = acc;
+        }
+        mx = colgroup_max(mx);
+        const float base = mx == kNegInf ? 0.f : mx;
+        float sum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum += fast_exp2(s[kt][i] - base);
+        sum = colgroup_sum(sum);
+        // no usable key: P = 0 everywhere (dQ = 0); lse stays -inf
+        const float lse = mx == kNegInf ? kNegInf : base + __builtin_log2f(sum);
+        const float lsub = mx == kNegInf ? 0.f : lse;
+        if (g == 0) lds_st4(slse + qrow * 4, __builtin_bit_cast(uint32_t, lse));
+        const float delta = __builtin_bit_cast(float, lds_ld4(sdelta + qrow * 4));
+        // dP^T = V dO^T, dS^T = P^T (dP^T - delta), packed per 32-key chunk
+        u32x4 dsk[NKC];
+#pragma unroll
+        for (int c = 0; c < NKC; ++c) {
+            float ds[8];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int kt = 2 * c + hh;
+                f32x4 dp = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < NI; ++i) dp = M::mma(ld_op(sv + kt * 16 * RS, i), doop[i], dp);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    ds[4 * hh + i] = keep_bit(fast_exp2(s[kt][i] - lsub) * (dp[i] - delta), ok, 4 * kt + i);
+            }
+            dsk[c] = u32x4{M::pack2(ds[0], ds[1]), M::pack2(ds[2], ds[3]), M::pack2(ds[4], ds[5]), M::pack2(ds[6], ds[7])};
+        }
+        // dQ^T = K^T dS^T
+        f32x4 dq[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NKC; ++c) {
+                const u32x2 lo = lds_ld8_tr16(sk + 32 * c * RS + troff[dt]);
+                const u32x2 hi = lds_ld8_tr16(sk + (32 * c + 16) * RS + troff[dt]);
+                acc = M::mma(u32x4{lo[0], lo[1], hi[0], hi[1]}, dsk[c], acc);
+            }
+            dq[dt] = acc;
+        }
+        store_row(rdq, a.dqss, qrow, dq, a.scale);
+    }
+    __syncthreads();  // log-sum-exp of every query is in LDS
+
+    // ---- phase 2: one 16-key tile per wave pass ----------------------------
+    for (int kt = wave; kt < NKT; kt += kWaves) {
+        const int key = kt * 16 + m;
+        const bool kok = key < a.Skv && !(prow && prow[key]);
+        const lds_t* const kbase = sk + kt * 16 * RS;
+        const lds_t* const vbase = sv + kt * 16 * RS;
+        u32x4 kop[NI], vop[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            kop[i] = ld_op(kbase, i);
+            vop[i] = ld_op(vbase, i);
+        }
+        f32x4 dvt[NDT], dkt[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) dvt[dt] = dkt[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int qp = 0; qp < nqp; ++qp) {
+            float p[8], ds[8];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int qt = 2 * qp + hh;
+                // S = Q K^T and dP = dO V^T: rows = queries qt*16 + 4g + i, column = key
+                f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f}, dpacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < NI; ++i) {
+                    sacc = M::mma(ld_op(sq + qt * 16 * RS, i), kop[i], sacc);
+                    dpacc = M::mma(ld_op(sdo + qt * 16 * RS, i), vop[i], dpacc);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int q = qt * 16 + 4 * g + i;
+                    const bool ok = kok && q < a.Sq && (!a.causal || key <= q);
+                    const float lse = __builtin_bit_cast(float, lds_ld4(slse + q * 4));
+                    const float delta = __builtin_bit_cast(float, lds_ld4(sdelta + q * 4));
+                    const float pv = fast_exp2(sacc[i] * a.c2 - lse);
+                    // 0 * lse: NaN only for a query that sees no key (lse = -inf)
+                    p[4 * hh + i] = ok ? pv : 0.f * lse;
+                    ds[4 * hh + i] = ok ? pv * (dpacc[i] - delta) : 0.f;
+                }
+            }
+            const u32x4 pb = {M::pack2(p[0], p[1]), M::pack2(p[2], p[3]), M::pack2(p[4], p[5]), M::pack2(p[6], p[7])};
+            const u32x4 db = {M::pack2(ds[0], ds[1]), M::pack2(ds[2], ds[3]), M::pack2(ds[4], ds[5]), M::pack2(ds[6], ds[7])};
+            // dV^T += dO^T P,  dK^T += Q^T dS over the 32 queries of the pair
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const u32x2 dlo = lds_ld8_tr16(sdo + 32 * qp * RS + troff[dt]);
+                const u32x2 dhi = lds_ld8_tr16(sdo + (32 * qp + 16) * RS + troff[dt]);
+                dvt[dt] = M::mma(u32x4{dlo[0], dlo[1], dhi[0], dhi[1]}, pb, dvt[dt]);
+                const u32x2 qlo = lds_ld8_tr16(sq + 32 * qp * RS + troff[dt]);
+                const u32x2 qhi = lds_ld8_tr16(sq + (32 * qp + 16) * RS + troff[dt]);
+                dkt[dt] = M::mma(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]}, db, dkt[dt]);
+            }
+        }
+        store_row(rdv, a.dvss, key, dvt, 1.0f);
+        store_row(rdk, a.dkss, key, dkt, a.scale);
+    }
+}
+
+namespace {
+
+template <typename K>
+int launch_bwd(K kernel, int grid, size_t lds, hipStream_t st, const BwdArgs& a) {
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) ATX_FAIL(ATX_ERR_LAUNCH, "hipFuncSetAttribute(%zu bytes LDS): %s", lds, hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), lds, st, a);
+    ATX_CHECK_LAUNCH("atx_attn_bwd launch");
+    return ATX_OK;
+}
+
+template <typename T, int D>
+int dispatch_bwd_nkc(int nkc, int grid, size_t lds, hipStream_t st, const BwdArgs& a) {
+    switch (nkc) {
+        case 1: return launch_bwd(attn_bwd_16bit<T, D, 1>, grid, lds, st, a);
+        case 2: return launch_bwd(attn_bwd_16bit<T, D, 2>, grid, lds, st, a);
+        case 3: return launch_bwd(attn_bwd_16bit<T, D, 3>, grid, lds, st, a);
+        case 4: return launch_bwd(attn_bwd_16bit<T, D, 4>, grid, lds, st, a);
+        case 5: return launch_bwd(attn_bwd_16bit<T, D, 5>, grid, lds, st, a);
+        case 6: return launch_bwd(attn_bwd_16bit<T, D, 6>, grid, lds, st, a);
+        case 7: return launch_bwd(attn_bwd_16bit<T, D, 7>, grid, lds, st, a);
+        case 8: return launch_bwd(attn_bwd_16bit<T, D, 8>, grid, lds, st, a);
+        default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_bwd: seq_kv needs %d 32-key chunks (<= 8)", nkc);
+    }
+}
+
+template <typename T>
+int dispatch_bwd(int D, int nkc, int grid, size_t lds, hipStream_t st, const BwdArgs& a) {
+    switch (D) {
+        case 16: return dispatch_bwd_nkc<T, 16>(nkc, grid, lds, st, a);
+        case 32: return dispatch_bwd_nkc<T, 32>(nkc, grid, lds, st, a);
+        case 48: return dispatch_bwd_nkc<T, 48>(nkc, grid, lds, st, a);
+        case 64: return dispatch_bwd_nkc<T, 64>(nkc, grid, lds, st, a);
+        case 80: return dispatch_bwd_nkc<T, 80>(nkc, grid, lds, st, a);
+        case 96: return dispatch_bwd_nkc<T, 96>(nkc, grid, lds, st, a);
+        case 112: return dispatch_bwd_nkc<T, 112>(nkc, grid, lds, st, a);
+        case 128: return dispatch_bwd_nkc<T, 128>(nkc, grid, lds, st, a);
+        default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_bwd: head_dim %d not supported", D);
+    }
+}
+
+bool rows16(const void* base, int64_t sb, int64_t ss, int64_t sh) {
+    return aligned16(base) && ((sb * 2) & 15) == 0 && ((ss * 2) & 15) == 0 && ((sh * 2) & 15) == 0;
+}
+
+}  // namespace
+}  // namespace atx
+
+extern "C" int atx_attn_bwd(const AtxAttnBwdParams* p, void* stream) {
+    using namespace atx;
+    clear_error();
+    if (!p) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_bwd: params is NULL");
+    if (p->abi_version != ATX_ABI_VERSION)
+        ATX_FAIL(ATX_ERR_ABI, "atx_attn_bwd: abi_version %d, library is %d", p->abi_version, ATX_ABI_VERSION);
+    if (p->dtype != ATX_DTYPE_BF16 && p->dtype != ATX_DTYPE_FP16) {
+        if (p->dtype == ATX_DTYPE_FP32) ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_bwd: fp32 is not supported");
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_bwd: unknown dtype %d", p->dtype);
+    }
+    if (p->batch < 1 || p->seq_q < 1 || p->seq_kv < 1 || p->num_heads < 1 || p->num_kv_heads < 1 || p->head_dim < 1)
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_bwd: sizes must be >= 1");
+    if (p->num_kv_heads != p->num_heads)
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_bwd: num_kv_heads %d != num_heads %d (GQA) not supported",
+                 p->num_kv_heads, p->num_heads);
+    if (!p->q || !p->k || !p->v || !p->o || !p->d_o || !p->dq || !p->dk || !p->dv)
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_bwd: null tensor pointer");
+    if (!(p->scale > 0.f) || p->scale == __builtin_inff())
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_bwd: scale must be finite and > 0 (got %g)", (double)p->scale);
+    if (p->head_dim % 16 != 0 || p->head_dim > 128)
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_bwd: head_dim %d not supported (multiple of 16, <= 128)", p->head_dim);
+    if (p->seq_q > 256 || p->seq_kv > 256)
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_bwd: seq_q %d / seq_kv %d not supported (<= 256)", p->seq_q, p->seq_kv);
+    const int64_t grid = (int64_t)p->batch * p->num_heads;
+    if (grid > 0x7fffffff) ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_bwd: batch*heads too large");
+    // Sequence strides of length-1 sequences are never used.
+    auto sstride = [](int64_t s, int seq, int d) { return seq == 1 ? (int64_t)d : s; };
+    const int D = p->head_dim;
+    const int64_t qss = sstride(p->q_stride_s, p->seq_q, D), oss = sstride(p->o_stride_s, p->seq_q, D);
+    const int64_t doss = sstride(p->do_stride_s, p->seq_q, D), dqss = sstride(p->dq_stride_s, p->seq_q, D);
+    const int64_t kss = sstride(p->k_stride_s, p->seq_kv, D), vss = sstride(p->v_stride_s, p->seq_kv, D);
+    const int64_t dkss = sstride(p->dk_stride_s, p->seq_kv, D), dvss = sstride(p->dv_stride_s, p->seq_kv, D);
+    if (!rows16(p->q, p->q_stride_b, qss, p->q_stride_h) || !rows16(p->k, p->k_stride_b, kss, p->k_stride_h) ||
+        !rows16(p->v, p->v_stride_b, vss, p->v_stride_h) || !rows16(p->o, p->o_stride_b, oss, p->o_stride_h) ||
+        !rows16(p->d_o, p->do_stride_b, doss, p->do_stride_h) ||
+        !rows16(p->dq, p->dq_stride_b, dqss, p->dq_stride_h) ||
+        !rows16(p->dk, p->dk_stride_b, dkss, p->dk_stride_h) || !rows16(p->dv, p->dv_stride_b, dvss, p->dv_stride_h))
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_bwd: every row must start on a 16-byte boundary");
+    // one (batch, head) slice per descriptor: 32-bit offsets, rows up to the
+    // next multiple of 32 past the end; output rows must not overlap
+    const int64_t strides_q[] = {qss, oss, doss, dqss}, strides_k[] = {kss, vss, dkss, dvss};
+    for (int64_t s : strides_q)
+        if (s < 0 || (p->seq_q + 32) * s * 2 + D * 2 > 0x7fffffffLL)
+            ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_bwd: sequence strides must be >= 0 and one slice < 2 GiB");
+    for (int64_t s : strides_k)
+        if (s < 0 || (p->seq_kv + 32) * s * 2 + D * 2 > 0x7fffffffLL)
+            ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_bwd: sequence strides must be >= 0 and one slice < 2 GiB");
+    if (dqss < D || dkss < D || dvss < D)
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_attn_bwd: gradient rows overlap");
+
+    const int nkc = (p->seq_kv + 31) / 32;
+    const int rk = nkc * 32, rq = ((p->seq_q + 31) / 32) * 32;
+    const size_t lds = bwd_lds_bytes(D, rk, rq);
+    if (lds > 160 * 1024)
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_attn_bwd: seq_q %d, seq_kv %d, head_dim %d need %zu bytes of LDS (> 160 KiB)",
+                 p->seq_q, p->seq_kv, D, lds);
+
+    BwdArgs a;
+    a.q = p->q; a.k = p->k; a.v = p->v; a.o = p->o; a.dout = p->d_o;
+    a.dq = p->dq; a.dk = p->dk; a.dv = p->dv;
+    a.qsb = p->q_stride_b; a.qsh = p->q_stride_h; a.ksb = p->k_stride_b; a.ksh = p->k_stride_h;
+    a.vsb = p->v_stride_b; a.vsh = p->v_stride_h; a.osb = p->o_stride_b; a.osh = p->o_stride_h;
+    a.dosb = p->do_stride_b; a.dosh = p->do_stride_h; a.dqsb = p->dq_stride_b; a.dqsh = p->dq_stride_h;
+    a.dksb = p->dk_stride_b; a.dksh = p->dk_stride_h; a.dvsb = p->dv_stride_b; a.dvsh = p->dv_stride_h;
+    a.qss = (int)qss; a.kss = (int)kss; a.vss = (int)vss; a.oss = (int)oss;
+    a.doss = (int)doss; a.dqss = (int)dqss; a.dkss = (int)dkss; a.dvss = (int)dvss;
+    a.kpad = p->key_pad;
+    a.kpsb = p->key_pad_stride_b;
+    a.H = p->num_heads;
+    a.Sq = p->seq_q;
+    a.Skv = p->seq_kv;
+    a.c2 = p->scale * kLog2e;
+    a.scale = p->scale;
+    a.causal = p->causal != 0;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (p->dtype == ATX_DTYPE_BF16) return dispatch_bwd<__bf16>(D, nkc, (int)grid, lds, st, a);
+    return dispatch_bwd<_Float16>(D, nkc, (int)grid, lds, st, a);
+}

@@ -150,6 +150,9 @@ __device__ inline void buf_st16(rsrc_t r, uint32_t off, u32x4 v) {
 __device__ inline void buf_st16_cached(rsrc_t r, uint32_t off, u32x4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, 0);
 }
+__device__ inline void buf_st8_cached(rsrc_t r, uint32_t off, u32x2 v) {
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, (int)off, 0, 0);
+}
 __device__ inline void buf_st4_cached(rsrc_t r, uint32_t off, uint32_t v) {
     __builtin_amdgcn_raw_buffer_store_b32(v, r, (int)off, 0, 0);
 }

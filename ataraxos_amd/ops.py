@@ -8,6 +8,8 @@ outside the kernels' range raises.
 * :func:`attention` — fused ``softmax(Q K^T * scale + mask) V`` on BSHD views
   (the seam ``_forward_<backend>(q, k, v, is_causal)`` of
   ``stratego/networks/attention.py:222-316``), differentiable.
+* :func:`attention_backward` — its dQ, dK, dV in one launch (the gradient
+  ``stratego/training/move_trainer.py:140`` takes through that attention).
 * :func:`kq_policy` — the key-query policy head's logits, legal-move mask and
   softmax (``stratego/networks/move_net.py:92-95`` plus the callers' softmax,
   ``stratego/training/selfplay.py:284``).
@@ -54,6 +56,17 @@ def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
+def _padding_bytes(key_padding_mask: torch.Tensor | None, b: int, skv: int, ref: torch.Tensor):
+    if key_padding_mask is None:
+        return None
+    if tuple(key_padding_mask.shape) != (b, skv):
+        raise ValueError(f"attention: key_padding_mask must be [{b}, {skv}]")
+    _require_device("attention", ref, key_padding_mask)
+    # bool and uint8 share one byte per element: reinterpret, no copy
+    return (key_padding_mask.view(torch.uint8) if key_padding_mask.dtype == torch.bool
+            else (key_padding_mask != 0).view(torch.uint8)).contiguous()
+
+
 def attention_supported(head_dim: int, seq_kv: int, dtype: torch.dtype) -> bool:
     """True when :func:`attention` covers this shape and dtype."""
     return dtype in _DTYPES and head_dim in HEAD_DIMS and 1 <= seq_kv <= MAX_SEQ_KV
@@ -90,14 +103,7 @@ def attention_forward(
         out = torch.empty((b, sq, h, d), dtype=q.dtype, device=q.device)
     elif tuple(out.shape) != (b, sq, h, d) or out.dtype != q.dtype or out.device != q.device:
         raise ValueError("attention: out has the wrong shape, dtype or device")
-    pad = None
-    if key_padding_mask is not None:
-        if tuple(key_padding_mask.shape) != (b, skv):
-            raise ValueError(f"attention: key_padding_mask must be [{b}, {skv}]")
-        _require_device("attention", q, key_padding_mask)
-        # bool and uint8 share one byte per element: reinterpret, no copy
-        pad = (key_padding_mask.view(torch.uint8) if key_padding_mask.dtype == torch.bool
-               else (key_padding_mask != 0).view(torch.uint8)).contiguous()
+    pad = _padding_bytes(key_padding_mask, b, skv, q)
     if scale is None:
         scale = 1.0 / math.sqrt(d)
 
@@ -135,20 +141,107 @@ def _attention_reference_fp32(q, k, v, causal, scale, key_padding_mask):
     return torch.matmul(torch.softmax(s, dim=-1), vh).transpose(1, 2)
 
 
+_BWD_DTYPES = (torch.bfloat16, torch.float16)
+_LDS_BYTES = 160 * 1024
+
+
+def _bwd_lds_bytes(head_dim: int, seq_q: int, seq_kv: int) -> int:
+    """LDS of one backward workgroup: K, V (S_kv rounded up to 32 rows), Q,
+    dO (S_q rounded up to 32 rows), and per query the log-sum-exp, delta and
+    head_dim/8 partial dot products (fp32)."""
+    rs = head_dim * 2 if head_dim in (64, 128) else head_dim * 2 + 16
+    rk = -(-seq_kv // 32) * 32
+    rq = -(-seq_q // 32) * 32
+    return (2 * rk + 2 * rq) * rs + rq * 4 * (2 + head_dim // 8)
+
+
+def attention_backward_supported(
+    head_dim: int, seq_q: int, seq_kv: int, num_heads: int, num_kv_heads: int, dtype: torch.dtype
+) -> bool:
+    """True when :func:`attention_backward` covers this shape and dtype:
+    bf16/fp16, no GQA, head_dim a multiple of 16 up to 128, both sequences
+    up to 256 and the workgroup's tiles within 160 KiB of LDS."""
+    return (
+        dtype in _BWD_DTYPES
+        and num_heads == num_kv_heads
+        and head_dim % 16 == 0
+        and 16 <= head_dim <= 128
+        and 1 <= seq_q <= MAX_SEQ_KV
+        and 1 <= seq_kv <= MAX_SEQ_KV
+        and _bwd_lds_bytes(head_dim, seq_q, seq_kv) <= _LDS_BYTES
+    )
+
+
+def attention_backward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    out: torch.Tensor,
+    grad_out: torch.Tensor,
+    causal: bool = False,
+    scale: float | None = None,
+    key_padding_mask: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradients ``(dq, dk, dv)`` of :func:`attention_forward` for the
+    upstream gradient ``grad_out``, given its inputs and its output ``out``
+    (all ``[B, S, H, D]``, bf16 or fp16).  One kernel launch; the softmax is
+    recomputed from Q and K, so nothing but the output is kept from the
+    forward.  Returns contiguous tensors in the inputs' dtype."""
+    _require_device("attention_backward", q, k, v, out, grad_out)
+    if not (q.dtype == k.dtype == v.dtype == out.dtype == grad_out.dtype):
+        raise ValueError("attention_backward: mixed dtypes")
+    b, sq, h, d = q.shape
+    skv, hkv = k.shape[1], k.shape[2]
+    if (tuple(k.shape) != (b, skv, hkv, d) or tuple(v.shape) != (b, skv, hkv, d)
+            or tuple(out.shape) != (b, sq, h, d) or tuple(grad_out.shape) != (b, sq, h, d)):
+        raise ValueError("attention_backward: shape mismatch")
+    if not attention_backward_supported(d, sq, skv, h, hkv, q.dtype):
+        raise NotImplementedError(
+            f"attention_backward: {q.dtype}, heads {h}/{hkv}, head_dim {d}, seq {sq}x{skv} not covered by the kernel"
+        )
+    q, k, v, out, grad_out = (_aligned_rows(t) for t in (q, k, v, out, grad_out))
+    pad = _padding_bytes(key_padding_mask, b, skv, q)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    dq = torch.empty((b, sq, h, d), dtype=q.dtype, device=q.device)
+    dk = torch.empty((b, skv, h, d), dtype=q.dtype, device=q.device)
+    dv = torch.empty((b, skv, h, d), dtype=q.dtype, device=q.device)
+
+    p = _lib.AttnBwdParams()
+    p.abi_version = _lib.ABI_VERSION
+    p.dtype = _DTYPES[q.dtype]
+    p.batch, p.seq_q, p.seq_kv, p.num_heads, p.num_kv_heads, p.head_dim = b, sq, skv, h, hkv, d
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", out), ("do", grad_out), ("dq", dq), ("dk", dk), ("dv", dv)):
+        setattr(p, "d_o" if name == "do" else name, t.data_ptr())
+        for axis, stride in zip("bsh", t.stride()[:3]):
+            setattr(p, f"{name}_stride_{axis}", stride)
+    p.scale = float(scale)
+    p.causal = 1 if causal else 0
+    p.key_pad = pad.data_ptr() if pad is not None else None
+    p.key_pad_stride_b = pad.stride(0) if pad is not None else 0
+    _lib.check(_lib.call("atx_attn_bwd", p, _stream(q)), "atx_attn_bwd")
+    return dq, dk, dv
+
+
 class _HipAttention(torch.autograd.Function):
-    """HIP forward; the backward recomputes the attention in fp32 with torch
-    ops on the same device and differentiates that."""
+    """HIP forward and, for bf16/fp16 without GQA, HIP backward
+    (:func:`attention_backward`).  fp32 inputs and GQA take their gradients
+    from an fp32 recomputation with torch ops on the same device."""
 
     @staticmethod
     def forward(ctx, q, k, v, causal, scale, key_padding_mask):  # type: ignore[override]
         out = attention_forward(q, k, v, causal=causal, scale=scale, key_padding_mask=key_padding_mask)
-        ctx.save_for_backward(q, k, v)
+        ctx.save_for_backward(q, k, v, out)
         ctx.causal, ctx.scale, ctx.kpm = causal, scale, key_padding_mask
         return out
 
     @staticmethod
     def backward(ctx, grad_out):  # type: ignore[override]
-        q, k, v = ctx.saved_tensors
+        q, k, v, out = ctx.saved_tensors
+        b, sq, h, d = q.shape
+        if attention_backward_supported(d, sq, k.shape[1], h, k.shape[2], q.dtype):
+            dq, dk, dv = attention_backward(q, k, v, out, grad_out.to(q.dtype), ctx.causal, ctx.scale, ctx.kpm)
+            return dq, dk, dv, None, None, None
         with torch.enable_grad():
             qf = q.detach().float().requires_grad_(True)
             kf = k.detach().float().requires_grad_(True)

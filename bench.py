@@ -24,6 +24,7 @@ roofline = 18.2 M samples/s).  Also reported on the same line:
 * ``belief_attention``: the attention kernel at the config C4 shapes
   (encoder self, decoder causal self, decoder cross with key padding);
 * ``decode``: the KV-cache decode kernel over config C5's 4 layers x 40 steps;
+* ``backward``: the attention backward kernel (dQ, dK, dV) of one C3 layer;
 * ``cpu_baseline``: the reference's math path (torch on the host CPU) on a
   bounded sample of the same layer, rank 0 only.
 
@@ -59,7 +60,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--qkv", choices=("separate", "packed"), default="separate",
                     help="q/k/v as three tensors or as views of one fused [B, L, 3E] projection")
-    ap.add_argument("--no-extras", action="store_true", help="skip the e2e, kq_policy, belief_attention and decode legs")
+    ap.add_argument("--no-extras", action="store_true", help="skip the e2e, kq_policy, belief_attention, decode and backward legs")
     ap.add_argument("--cpu-sample", type=int, default=1024, help="batch of the CPU baseline sample")
     ap.add_argument(
         "--mode",
@@ -293,6 +294,24 @@ def time_decode(torch, ops, dev, reps):
             "achieved_gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "bytes_per_sequence": nbytes}
 
 
+def time_backward(torch, ops, batch, dev, steps, warmup):
+    """Backward of the C3 attention layer (B=4096, L=100, 6 x 64, bf16): the
+    gradient the Move trainer takes through attention.  Q, K, V, the forward
+    output O and dO are resident; one launch writes dQ, dK, dV."""
+    g = torch.Generator(device=dev).manual_seed(48)
+    s, h, d = 100, 6, 64
+    q, k, v, do = (torch.randn(batch, s, h, d, generator=g, device=dev).to(torch.bfloat16) for _ in range(4))
+    o = ops.attention_forward(q, k, v)
+    ms = _mean_launch_ms(torch, lambda: ops.attention_backward(q, k, v, o, do), steps, warmup)
+    nbytes = batch * h * 8 * s * d * 2  # Q, K, V, O, dO read; dQ, dK, dV written
+    flops = batch * h * 5 * 2 * s * s * d  # S recomputed, dP, dV, dQ, dK
+    leg = _leg("attention backward, C3 layer", ms, nbytes, batch)
+    leg.update({"config": "C3 layer backward, B=4096, L=100, 6x64, bf16", "kernel": "attn_bwd_16bit<bf16, D=64, NKC=4>",
+                "algorithmic_bytes_per_launch": nbytes, "tflops": flops / (ms * 1e-3) / 1e12,
+                "mfma_frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS})
+    return leg
+
+
 def cpu_baseline(sample: int) -> dict:
     from oracle.cpu_baseline import attention_baseline
 
@@ -408,6 +427,7 @@ def main() -> int:
         result["kq_policy"] = time_kq(torch, ops, batch, dev, args.steps, args.warmup)
         result["belief_attention"] = time_belief(torch, ops, dev, args.steps, args.warmup)
         result["decode"] = time_decode(torch, ops, dev, max(3, args.steps // 10))
+        result["backward"] = time_backward(torch, ops, batch, dev, args.steps, args.warmup)
         print("[bench] extras timed", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_sample)

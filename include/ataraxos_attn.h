@@ -104,6 +104,52 @@ typedef struct AtxAttnParams {
  */
 int atx_attn_fwd(const AtxAttnParams* params, void* stream);
 
+/* Gradients of atx_attn_fwd: given Q, K, V, the forward output O and dO, write
+ * dQ, dK, dV (same [B, S, H, D] layouts as their tensors). */
+typedef struct AtxAttnBwdParams {
+    int32_t abi_version; /* must equal ATX_ABI_VERSION */
+    int32_t dtype;       /* ATX_DTYPE_BF16 or ATX_DTYPE_FP16: every tensor has this type */
+    int32_t batch;
+    int32_t seq_q;
+    int32_t seq_kv;
+    int32_t num_heads;    /* H */
+    int32_t num_kv_heads; /* must equal H */
+    int32_t head_dim;     /* D */
+    const void* q;
+    int64_t q_stride_b, q_stride_s, q_stride_h;
+    const void* k;
+    int64_t k_stride_b, k_stride_s, k_stride_h;
+    const void* v;
+    int64_t v_stride_b, v_stride_s, v_stride_h;
+    const void* o;
+    int64_t o_stride_b, o_stride_s, o_stride_h;
+    const void* d_o;
+    int64_t do_stride_b, do_stride_s, do_stride_h;
+    void* dq;
+    int64_t dq_stride_b, dq_stride_s, dq_stride_h;
+    void* dk;
+    int64_t dk_stride_b, dk_stride_s, dk_stride_h;
+    void* dv;
+    int64_t dv_stride_b, dv_stride_s, dv_stride_h;
+    float scale;
+    int32_t causal;
+    const uint8_t* key_pad; /* optional [batch, seq_kv]; nonzero = ignore key */
+    int64_t key_pad_stride_b;
+} AtxAttnBwdParams;
+
+/*
+ * Replaces the autograd backward of the attention the reference trains
+ * through (stratego/training/move_trainer.py:140 -> MultiHeadAttention.forward,
+ * stratego/networks/attention.py:281-316 on the math path, or FA3 / FA2 /
+ * SDPA's own backward).  The softmax is recomputed from Q and K.
+ *
+ * Supported range: BF16 / FP16; num_kv_heads == num_heads; head_dim a
+ * multiple of 16 up to 128; 1 <= seq_q, seq_kv <= 256.  Gradients of key
+ * padded or causally masked entries are zero; a query row with no usable key
+ * gets dQ = 0.
+ */
+int atx_attn_bwd(const AtxAttnBwdParams* params, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Key-query policy head: logits + legal-move mask (+ softmax)              */
 /* ------------------------------------------------------------------------ */

@@ -10,7 +10,8 @@ Modules (each function cites the reference file:line it restates):
 
 * :mod:`oracle.attention` — numpy float64 restatement of
   ``MultiHeadAttention._forward_math`` (stratego/networks/attention.py:281-316),
-  the GQA expansion (:210-220) and the module forward (:152-204).
+  the GQA expansion (:210-220) and the module forward (:152-204), and the
+  gradients autograd takes through that math (stratego/training/move_trainer.py:140).
 * :mod:`oracle.policy` — the key-query policy head's logits and mask
   (stratego/networks/move_net.py:89-95) and the callers' softmax
   (stratego/training/selfplay.py:284).
@@ -23,7 +24,8 @@ Pinning.  The reference holds no golden values for this path (its tests check
 invariants only), so every oracle function is pinned by checks in
 ``tests/test_oracle_*.py`` against results it does not share code with:
 torch's ``scaled_dot_product_attention`` and ``nn.MultiheadAttention`` on the
-CPU in float64, scipy's ``softmax``, closed forms (one key, constant keys,
+CPU in float64 (and torch autograd through them for the gradients), central
+finite differences of the forward, scipy's ``softmax``, closed forms (one key, constant keys,
 one dominant logit, causal row 0, a single legal move, equal logits), the
 reference's own invariants, and planted-mistake tests showing that each
 check rejects a wrong variant.  No function here is "parity unpinned".

@@ -69,6 +69,62 @@ def attention(
     return np.matmul(softmax_lastdim(scores), v64).transpose(0, 2, 1, 3)
 
 
+def attention_backward(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    d_o: np.ndarray,
+    causal: bool = False,
+    scale: float | None = None,
+    key_pad: np.ndarray | None = None,
+) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Gradients ``(dq, dk, dv)`` of :func:`attention` for the upstream
+    gradient ``d_o`` (``[B, S_q, H, D]``), in float64.
+
+    This is what autograd takes through ``_forward_math``
+    (stratego/networks/attention.py:281-316) when the training step calls
+    ``backward`` (stratego/training/move_trainer.py:140), written out by the
+    chain rule: ``O = P V`` gives ``dV = P^T dO`` and ``dP = dO V^T``; the
+    softmax over keys (:310) gives ``dS = P * (dP - rowsum(dP * P))``; the
+    post-product scale (:300-301) gives ``dQ = scale dS K`` and
+    ``dK = scale dS^T Q``.  The mask is applied with ``masked_fill``
+    (:303-308), whose gradient is 0 at masked scores, so ``dS = 0`` there.
+    The GQA expansion (:210-220) sums the gradients of the ``H / H_kv`` query
+    heads that share a KV head.  An all-masked row has ``P = NaN`` (as in the
+    forward): its ``dS`` is still 0 (every entry is masked), so it adds 0 to
+    ``dq`` and ``dk``, but ``dV = P^T dO`` makes the whole ``(batch, head)``
+    slice of ``dv`` NaN -- what autograd through that math gives.
+    """
+    q64 = np.asarray(q, dtype=np.float64).transpose(0, 2, 1, 3)
+    k64 = np.asarray(k, dtype=np.float64).transpose(0, 2, 1, 3)
+    v64 = np.asarray(v, dtype=np.float64).transpose(0, 2, 1, 3)
+    g64 = np.asarray(d_o, dtype=np.float64).transpose(0, 2, 1, 3)
+    b, num_heads, seq_q, head_dim = q64.shape
+    kv_heads, seq_kv = k64.shape[1], k64.shape[2]
+    ke = expand_kv_heads(k64, num_heads)
+    ve = expand_kv_heads(v64, num_heads)
+    if scale is None:
+        scale = 1.0 / np.sqrt(head_dim)
+    scores = np.matmul(q64, ke.swapaxes(-1, -2)) * scale
+    masked = np.zeros((1, 1, seq_q, seq_kv), dtype=bool)
+    if causal:
+        masked = masked | np.triu(np.ones((seq_q, seq_kv), dtype=bool), 1)
+    if key_pad is not None:
+        masked = masked | np.asarray(key_pad, dtype=bool)[:, None, None, :]
+    p = softmax_lastdim(np.where(masked, NEG_INF, scores))
+    with np.errstate(invalid="ignore"):
+        dv = np.matmul(p.swapaxes(-1, -2), g64)
+        dp = np.matmul(g64, ve.swapaxes(-1, -2))
+        ds = np.where(masked, 0.0, p * (dp - np.sum(dp * p, axis=-1, keepdims=True)))
+        dq = np.matmul(ds, ke) * scale
+        dk = np.matmul(ds.swapaxes(-1, -2), q64) * scale
+    group = num_heads // kv_heads
+    if group > 1:
+        dk = dk.reshape(b, kv_heads, group, seq_kv, head_dim).sum(axis=2)
+        dv = dv.reshape(b, kv_heads, group, seq_kv, head_dim).sum(axis=2)
+    return dq.transpose(0, 2, 1, 3), dk.transpose(0, 2, 1, 3), dv.transpose(0, 2, 1, 3)
+
+
 def linear(x: np.ndarray, weight: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
     """``x W^T + b`` as ``torch.nn.Linear`` (weight ``[out, in]``)."""
     y = np.asarray(x, np.float64) @ np.asarray(weight, np.float64).T

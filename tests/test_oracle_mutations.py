@@ -13,7 +13,7 @@ import numpy as np
 import torch
 import torch.nn.functional as F  # noqa: N812
 
-from oracle.attention import attention, softmax_lastdim
+from oracle.attention import attention, attention_backward, softmax_lastdim
 from oracle.policy import kq_probs
 
 
@@ -95,3 +95,82 @@ def test_flatten_order_mistake_is_caught():
     q, k = rnd(1, 100, 64, seed=1), rnd(1, 100, 64, seed=2)
     assert kq_probs(q, k, mask, 1 / 8)[0, 3 * 100 + 5] == 1.0
     assert mutant_to_major_probs(q, k, mask, 1 / 8)[0, 3 * 100 + 5] == 0.0
+
+
+# --- backward ----------------------------------------------------------------
+
+
+def _bwd_parts(q, k, v, d_o):
+    """P, dP and the BHSD operands of a small unmasked case."""
+    qh, kh, vh, gh = (_bhsd(x) for x in (q, k, v, d_o))
+    scale = 1 / np.sqrt(q.shape[-1])
+    p = softmax_lastdim(qh @ kh.swapaxes(-1, -2) * scale)
+    return qh, kh, vh, gh, p, gh @ vh.swapaxes(-1, -2), scale
+
+
+def mutant_bwd_dropped_softmax_term(q, k, v, d_o):
+    """dS = P * dP: the rowsum(dP * P) term of the softmax gradient dropped."""
+    qh, kh, vh, gh, p, dp, scale = _bwd_parts(q, k, v, d_o)
+    ds = p * dp
+    return tuple(x.transpose(0, 2, 1, 3) for x in (ds @ kh * scale, ds.swapaxes(-1, -2) @ qh * scale,
+                                                   p.swapaxes(-1, -2) @ gh))
+
+
+def mutant_bwd_missing_scale(q, k, v, d_o):
+    """dQ = dS K without the post-product scale."""
+    dq, dk, dv = attention_backward(q, k, v, d_o)
+    return dq * np.sqrt(q.shape[-1]), dk, dv
+
+
+def mutant_bwd_untransposed_ds(q, k, v, d_o):
+    """dK = dS Q instead of dS^T Q (same shape when S_q = S_kv)."""
+    qh, kh, vh, gh, p, dp, scale = _bwd_parts(q, k, v, d_o)
+    ds = p * (dp - np.sum(dp * p, axis=-1, keepdims=True))
+    return tuple(x.transpose(0, 2, 1, 3) for x in (ds @ kh * scale, ds @ qh * scale, p.swapaxes(-1, -2) @ gh))
+
+
+def mutant_bwd_gqa_first_head(q, k, v, d_o):
+    """GQA: dk/dv taken from the first query head of each group instead of the sum."""
+    h, hkv = q.shape[2], k.shape[2]
+    dq, dk, dv = attention_backward(q, np.repeat(k, h // hkv, axis=2), np.repeat(v, h // hkv, axis=2), d_o)
+    return dq, dk[:, :, :: h // hkv], dv[:, :, :: h // hkv]
+
+
+def _fd_grads(q, k, v, d_o, eps=1e-6):
+    """Central finite differences of <attention(q, k, v), dO> (the pinning check)."""
+    out = []
+    for which in range(3):
+        x = [q, k, v]
+        g = np.zeros_like(x[which])
+        for idx in np.ndindex(*g.shape):
+            p_, m_ = [a.copy() for a in x], [a.copy() for a in x]
+            p_[which][idx] += eps
+            m_[which][idx] -= eps
+            g[idx] = (np.sum(attention(*p_) * d_o) - np.sum(attention(*m_) * d_o)) / (2 * eps)
+        out.append(g)
+    return out
+
+
+def test_backward_mistakes_are_caught_by_finite_differences():
+    q, k, v, d_o = rnd(1, 4, 2, 4, seed=1), rnd(1, 4, 2, 4, seed=2), rnd(1, 4, 2, 4, seed=3), rnd(1, 4, 2, 4, seed=4)
+    fd = _fd_grads(q, k, v, d_o)
+    for a, r in zip(attention_backward(q, k, v, d_o), fd):
+        np.testing.assert_allclose(a, r, rtol=1e-6, atol=1e-8)
+    for mutant in (mutant_bwd_dropped_softmax_term, mutant_bwd_missing_scale, mutant_bwd_untransposed_ds):
+        got = mutant(q, k, v, d_o)
+        assert not all(np.allclose(a, r, rtol=1e-4, atol=1e-6) for a, r in zip(got, fd)), mutant.__name__
+
+
+def test_backward_gqa_mistake_is_caught_by_torch_autograd():
+    q, k, v, d_o = rnd(2, 5, 8, 4, seed=1), rnd(2, 6, 2, 4, seed=2), rnd(2, 6, 2, 4, seed=3), rnd(2, 5, 8, 4, seed=4)
+    tk, tv = (torch.from_numpy(x).requires_grad_(True) for x in (k, v))
+    kh = tk.transpose(1, 2).repeat_interleave(4, 1)
+    vh = tv.transpose(1, 2).repeat_interleave(4, 1)
+    o = F.scaled_dot_product_attention(torch.from_numpy(q).transpose(1, 2), kh, vh).transpose(1, 2)
+    o.backward(torch.from_numpy(d_o))
+    ref = (tk.grad.numpy(), tv.grad.numpy())
+    _, dk, dv = attention_backward(q, k, v, d_o)
+    np.testing.assert_allclose(dk, ref[0], rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dv, ref[1], rtol=1e-10, atol=1e-12)
+    _, mk, mv = mutant_bwd_gqa_first_head(q, k, v, d_o)
+    assert not np.allclose(mk, ref[0], atol=1e-6) and not np.allclose(mv, ref[1], atol=1e-6)
