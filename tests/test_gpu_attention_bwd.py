@@ -10,8 +10,10 @@ bf16/fp16-rounded inputs.
 Tolerance.  The contract's figure for 16-bit results is 2e-2 max-abs on
 outputs of unit scale.  Gradients scale with the upstream gradient, so each
 one is held to ``max|g - ref| <= 2e-2 * max|ref|`` (normwise relative), plus
-``||g - ref||_F <= 1e-2 * ||ref||_F``.  NaNs (rows that see no key) must
-coincide exactly, and gradients of padded keys must be exactly 0.
+``||g - ref||_F <= 1e-2 * ||ref||_F``.  Where the exact gradient vanishes
+(``S_kv = 1`` makes dQ and dK 0 in exact arithmetic) ``max|ref|`` is floored at
+1e-4, i.e. an absolute 2e-6.  NaNs (rows that see no key) must coincide
+exactly, and gradients of padded keys must be exactly 0.
 """
 
 from __future__ import annotations
@@ -30,6 +32,7 @@ pytestmark = pytest.mark.gpu
 
 REL_MAX = 2e-2
 REL_FRO = 1e-2
+ZERO_FLOOR = 1e-4
 
 
 def _announce(msg: str) -> None:
@@ -45,11 +48,12 @@ def assert_grad_close(got: torch.Tensor, ref: np.ndarray, what: str) -> float:
     g, r = g[~nan_r], ref[~nan_r]
     if r.size == 0:
         return 0.0
-    scale = max(float(np.max(np.abs(r))), 1e-30)
+    scale = max(float(np.max(np.abs(r))), ZERO_FLOOR)
     err = float(np.max(np.abs(g - r)))
     assert err <= REL_MAX * scale, f"{what}: max-abs {err:.3e} > {REL_MAX} * {scale:.3e}"
-    fro = float(np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30))
-    assert fro <= REL_FRO, f"{what}: relative Frobenius error {fro:.3e} > {REL_FRO}"
+    if scale > ZERO_FLOOR:
+        fro = float(np.linalg.norm(g - r) / np.linalg.norm(r))
+        assert fro <= REL_FRO, f"{what}: relative Frobenius error {fro:.3e} > {REL_FRO}"
     return err / scale
 
 
@@ -77,8 +81,11 @@ def run_case(cuda, b, sq, skv, h, d, dtype, causal=False, pad_p=None, seed=0, st
                           key_pad=None if pad is None else pad.numpy())
     errs = [assert_grad_close(a, r, f"{n} b={b} sq={sq} skv={skv} d={d} {dtype}") for n, a, r in zip(("dq", "dk", "dv"), (dq, dk, dv), ref)]
     if pad is not None:
+        # exactly 0, except in a dv slice a row that sees no key made NaN
+        # (whose pattern was matched against the oracle above)
         padded = pad.to(cuda)[:, :, None, None].expand_as(dk)
-        assert (dk[padded] == 0).all() and (dv[padded] == 0).all(), "padded keys must get exactly 0"
+        assert (dk[padded] == 0).all(), "padded keys must get exactly 0 in dk"
+        assert ((dv[padded] == 0) | dv[padded].isnan()).all(), "padded keys must get exactly 0 in dv"
     return errs
 
 
@@ -163,9 +170,10 @@ def test_key_padding(cuda, causal, dtype):
 
 
 def test_large_head_dim_long_sequence(cuda):
-    """D=128 at the longest sequence whose tiles fit in LDS (S=160)."""
-    assert ops.attention_backward_supported(128, 160, 160, 2, 2, torch.bfloat16)
-    run_case(cuda, 2, 160, 160, 2, 128, torch.bfloat16, seed=90)
+    """D=128 at the longest sequence whose tiles fit in LDS (S=128)."""
+    assert ops.attention_backward_supported(128, 128, 128, 2, 2, torch.bfloat16)
+    assert not ops.attention_backward_supported(128, 129, 129, 2, 2, torch.bfloat16)
+    run_case(cuda, 2, 128, 128, 2, 128, torch.bfloat16, seed=90)
 
 
 def test_large_logits_are_stable(cuda):
