@@ -6,12 +6,13 @@
 //   dP = dO V^T,  dS = P * (dP - delta),
 //   dQ = scale * dS K,  dK = scale * dS^T Q,  dV = P^T dO.
 //
-// One workgroup (4 waves) per (batch, head), everything for that pair
+// One workgroup (8 waves) per (batch, head), everything for that pair
 // resident in LDS: K, V, Q and dO rows in one layout that serves both 16-byte
 // row reads and the transposing reads (ds_read_b64_tr_b16), plus the
 // per-query log-sum-exp and delta.
 //  * Phase 1, one wave per 16-query tile, in the forward's orientation
-//    (S^T = K Q^T: each lane owns one query): recompute the softmax and its
+//    (S^T = K Q^T: each lane owns one query): delta from the O tile (read
+//    straight into registers) and the dO tile, the softmax and its
 //    log-sum-exp, then dP^T = V dO^T, dS^T, and dQ^T = K^T dS^T with dS^T
 //    fed from registers the way the forward feeds P^T.
 //  * Phase 2, one wave per 16-key tile (S = Q K^T: each lane owns one key):
@@ -48,8 +49,8 @@ struct BwdArgs {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = 4;
+constexpr int kThreads = 512;
+constexpr int kWaves = 8;
 
 // Row layout shared by every staged matrix.  At D = 64 / 128 the 16-byte
 // chunk c of row r sits at c ^ ((r >> 1) & 7): the 16 rows of an MFMA operand
@@ -83,15 +84,24 @@ __device__ inline float keep_bit(float x, uint64_t bits, int bit) {
 
 }  // namespace
 
-// Bytes of LDS for one workgroup.
+// Bytes of LDS for one workgroup: K, V (rk rows), Q, dO (rq rows), and the
+// log-sum-exp and delta of rq queries.
 inline size_t bwd_lds_bytes(int D, int rk, int rq) {
     const int rs = (D == 64 || D == 128) ? D * 2 : D * 2 + 16;
-    return (size_t)(2 * rk + 2 * rq) * rs + (size_t)rq * 4 * (2 + D / 8);
+    return (size_t)(2 * rk + 2 * rq) * rs + (size_t)rq * 8;
+}
+
+// Waves per SIMD the register allocator is asked to fit: 4 lets two
+// 8-wave workgroups share a CU (128 VGPRs each), which the C3 shape's LDS
+// (66.5 KiB) allows; longer sequences keep more scores per lane.
+template <int D, int NKC>
+constexpr int bwd_occ() {
+    return (NKC <= 4 && D <= 64) ? 4 : 2;
 }
 
 // NKC = 32-key chunks (S_kv <= 32 * NKC).
 template <typename T, int D, int NKC>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(bwd_occ<D, NKC>(), 8)))
 void attn_bwd_16bit(BwdArgs a) {
     using M = Mfma16<T>;
     constexpr int CH = D / 8;          // 16-byte chunks per row
@@ -101,6 +111,7 @@ void attn_bwd_16bit(BwdArgs a) {
     constexpr int NKT = 2 * NKC;       // key tiles
     constexpr int RK = NKT * 16;       // K / V rows staged
     constexpr int RS = row_bytes<D>();
+    constexpr uint32_t kOut = 0xfffffff0u;  // a buffer offset past any slice: loads 0
 
     const int nqt = (a.Sq + 15) >> 4;
     const int nqp = (nqt + 1) >> 1;  // pairs of query tiles
@@ -110,9 +121,8 @@ void attn_bwd_16bit(BwdArgs a) {
     lds_t* const sv = sk + RK * RS;
     lds_t* const sq = sv + RK * RS;
     lds_t* const sdo = sq + RQ * RS;
-    lds_t* const slse = sdo + RQ * RS;  // RQ floats: log-sum-exp in log2 units
-    lds_t* const sdelta = slse + RQ * 4;  // RQ floats
-    lds_t* const spart = sdelta + RQ * 4;  // RQ x CH floats: partial dots of delta
+    lds_t* const slse = sdo + RQ * RS;    // RQ floats: log-sum-exp in log2 units
+    lds_t* const sdelta = slse + RQ * 4;  // RQ floats: rowsum(O * dO)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -134,7 +144,19 @@ void attn_bwd_16bit(BwdArgs a) {
     const rsrc_t rdk = slice(a.dk, a.dksb, a.dksh, a.dkss, a.Skv);
     const rsrc_t rdv = slice(a.dv, a.dvsb, a.dvsh, a.dvss, a.Skv);
 
-    // ---- stage K, V (RK rows), Q, dO (RQ rows); partial dots O . dO --------
+    // O rows of a query tile in the MFMA operand layout (row m, chunks 4i+g),
+    // for delta; chunks past the row read 0.
+    u32x4 oop[NI];
+    auto load_o = [&](int qt) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const bool in = CH % 4 == 0 || 4 * i + g < CH;
+            oop[i] = buf_ld16(ro, in ? (uint32_t)((qt * 16 + m) * a.oss + (4 * i + g) * 8) * 2 : kOut);
+        }
+    };
+    if (wave < nqt) load_o(wave);
+
+    // ---- stage K, V (RK rows), Q, dO (RQ rows) ------------------------------
     for (int idx = tid; idx < RK * CH; idx += kThreads) {
         const int r = idx / CH, c = idx - (idx / CH) * CH;
         lds_st16(sk + chunk_off<D>(r, c), buf_ld16(rk, (uint32_t)(r * a.kss + c * 8) * 2));
@@ -142,27 +164,13 @@ void attn_bwd_16bit(BwdArgs a) {
     }
     for (int idx = tid; idx < RQ * CH; idx += kThreads) {
         const int r = idx / CH, c = idx - (idx / CH) * CH;
-        const u32x4 qv = buf_ld16(rq, (uint32_t)(r * a.qss + c * 8) * 2);
-        const u32x4 dv = buf_ld16(rdo, (uint32_t)(r * a.doss + c * 8) * 2);
-        const u32x4 ov = buf_ld16(ro, (uint32_t)(r * a.oss + c * 8) * 2);
-        lds_st16(sq + chunk_off<D>(r, c), qv);
-        lds_st16(sdo + chunk_off<D>(r, c), dv);
-        float part = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            part = __builtin_fmaf(M::to_float((uint16_t)(ov[j] & 0xffffu)), M::to_float((uint16_t)(dv[j] & 0xffffu)), part);
-            part = __builtin_fmaf(M::to_float((uint16_t)(ov[j] >> 16)), M::to_float((uint16_t)(dv[j] >> 16)), part);
-        }
-        lds_st4(spart + idx * 4, __builtin_bit_cast(uint32_t, part));
+        lds_st16(sq + chunk_off<D>(r, c), buf_ld16(rq, (uint32_t)(r * a.qss + c * 8) * 2));
+        lds_st16(sdo + chunk_off<D>(r, c), buf_ld16(rdo, (uint32_t)(r * a.doss + c * 8) * 2));
     }
-    __syncthreads();
-    // delta_q: each row's partials summed in a fixed order.  The log-sum-exp
-    // starts at 0 for every staged row; phase 1 overwrites the rows it covers.
-    for (int r = tid; r < RQ; r += kThreads) {
-        float d = 0.f;
-        for (int c = 0; c < CH; ++c) d += __builtin_bit_cast(float, lds_ld4(spart + (r * CH + c) * 4));
-        lds_st4(sdelta + r * 4, __builtin_bit_cast(uint32_t, d));
+    // Rows of the last pair that no query tile covers: defined lse and delta.
+    for (int r = nqt * 16 + tid; r < RQ; r += kThreads) {
         lds_st4(slse + r * 4, 0u);
+        lds_st4(sdelta + r * 4, 0u);
     }
 
     // Usable keys of this lane in phase 1 (bit 4*kt + i <-> key 16*kt + 4g + i).
@@ -208,6 +216,14 @@ void attn_bwd_16bit(BwdArgs a) {
                                u32x2{M::pack2(x[dt][0] * mul, x[dt][1] * mul), M::pack2(x[dt][2] * mul, x[dt][3] * mul)});
         }
     };
+    auto dot8 = [&](u32x4 x, u32x4 y, float acc) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc = __builtin_fmaf(M::to_float((uint16_t)(x[j] & 0xffffu)), M::to_float((uint16_t)(y[j] & 0xffffu)), acc);
+            acc = __builtin_fmaf(M::to_float((uint16_t)(x[j] >> 16)), M::to_float((uint16_t)(y[j] >> 16)), acc);
+        }
+        return acc;
+    };
 
     // ---- phase 1: one 16-query tile per wave pass --------------------------
     for (int qt = wave; qt < nqt; qt += kWaves) {
@@ -220,6 +236,13 @@ void attn_bwd_16bit(BwdArgs a) {
             qop[i] = ld_op(qbase, i);
             doop[i] = ld_op(dobase, i);
         }
+        // delta = rowsum(O * dO) of this lane's query (the first tile's O
+        // was requested before the staging loads)
+        if (qt != wave) load_o(qt);
+        float part = 0.f;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) part = dot8(oop[i], doop[i], part);
+        const float delta = colgroup_sum(part);
         // usable keys of this query row
         uint64_t ok = kbits;
         if (a.causal) {
@@ -254,11 +277,13 @@ void attn_bwd_16bit(BwdArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) sum += fast_exp2(s[kt][i] - base);
         sum = colgroup_sum(sum);
-        // no usable key: P = 0 everywhere (dQ = 0); lse stays -inf
+        // no usable key: P = 0 everywhere here (dQ = 0); lse stays -inf
         const float lse = mx == kNegInf ? kNegInf : base + __builtin_log2f(sum);
         const float lsub = mx == kNegInf ? 0.f : lse;
-        if (g == 0) lds_st4(slse + qrow * 4, __builtin_bit_cast(uint32_t, lse));
-        const float delta = __builtin_bit_cast(float, lds_ld4(sdelta + qrow * 4));
+        if (g == 0) {
+            lds_st4(slse + qrow * 4, __builtin_bit_cast(uint32_t, lse));
+            lds_st4(sdelta + qrow * 4, __builtin_bit_cast(uint32_t, delta));
+        }
         // dP^T = V dO^T, dS^T = P^T (dP^T - delta), packed per 32-key chunk
         u32x4 dsk[NKC];
 #pragma unroll
@@ -291,7 +316,7 @@ void attn_bwd_16bit(BwdArgs a) {
         }
         store_row(rdq, a.dqss, qrow, dq, a.scale);
     }
-    __syncthreads();  // log-sum-exp of every query is in LDS
+    __syncthreads();  // log-sum-exp and delta of every query are in LDS
 
     // ---- phase 2: one 16-key tile per wave pass ----------------------------
     for (int kt = wave; kt < NKT; kt += kWaves) {
@@ -320,16 +345,16 @@ void attn_bwd_16bit(BwdArgs a) {
                     sacc = M::mma(ld_op(sq + qt * 16 * RS, i), kop[i], sacc);
                     dpacc = M::mma(ld_op(sdo + qt * 16 * RS, i), vop[i], dpacc);
                 }
+                const f32x4 lse4 = as_f32x4(lds_ld16(slse + (qt * 16 + 4 * g) * 4));
+                const f32x4 delta4 = as_f32x4(lds_ld16(sdelta + (qt * 16 + 4 * g) * 4));
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int q = qt * 16 + 4 * g + i;
                     const bool ok = kok && q < a.Sq && (!a.causal || key <= q);
-                    const float lse = __builtin_bit_cast(float, lds_ld4(slse + q * 4));
-                    const float delta = __builtin_bit_cast(float, lds_ld4(sdelta + q * 4));
-                    const float pv = fast_exp2(sacc[i] * a.c2 - lse);
+                    const float pv = fast_exp2(sacc[i] * a.c2 - lse4[i]);
                     // 0 * lse: NaN only for a query that sees no key (lse = -inf)
-                    p[4 * hh + i] = ok ? pv : 0.f * lse;
-                    ds[4 * hh + i] = ok ? pv * (dpacc[i] - delta) : 0.f;
+                    p[4 * hh + i] = ok ? pv : 0.f * lse4[i];
+                    ds[4 * hh + i] = ok ? pv * (dpacc[i] - delta4[i]) : 0.f;
                 }
             }
             const u32x4 pb = {M::pack2(p[0], p[1]), M::pack2(p[2], p[3]), M::pack2(p[4], p[5]), M::pack2(p[6], p[7])};

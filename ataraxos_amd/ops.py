@@ -147,12 +147,12 @@ _LDS_BYTES = 160 * 1024
 
 def _bwd_lds_bytes(head_dim: int, seq_q: int, seq_kv: int) -> int:
     """LDS of one backward workgroup: K, V (S_kv rounded up to 32 rows), Q,
-    dO (S_q rounded up to 32 rows), and per query the log-sum-exp, delta and
-    head_dim/8 partial dot products (fp32)."""
+    dO (S_q rounded up to 32 rows), and per query the log-sum-exp and delta
+    (fp32)."""
     rs = head_dim * 2 if head_dim in (64, 128) else head_dim * 2 + 16
     rk = -(-seq_kv // 32) * 32
     rq = -(-seq_q // 32) * 32
-    return (2 * rk + 2 * rq) * rs + rq * 4 * (2 + head_dim // 8)
+    return (2 * rk + 2 * rq) * rs + rq * 8
 
 
 def attention_backward_supported(
