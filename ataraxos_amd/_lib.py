@@ -93,6 +93,37 @@ class KqParams(ctypes.Structure):
     ]
 
 
+class KqBwdParams(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", _i32),
+        ("dtype", _i32),
+        ("batch", _i32),
+        ("seq", _i32),
+        ("dim", _i32),
+        ("out_mode", _i32),
+        ("q", _ptr),
+        ("q_stride_b", _i64),
+        ("q_stride_s", _i64),
+        ("k", _ptr),
+        ("k_stride_b", _i64),
+        ("k_stride_s", _i64),
+        ("mask", _ptr),
+        ("mask_stride_b", _i64),
+        ("mask_stride_s", _i64),
+        ("grad", _ptr),
+        ("grad_stride_b", _i64),
+        ("probs", _ptr),
+        ("probs_stride_b", _i64),
+        ("dq", _ptr),
+        ("dq_stride_b", _i64),
+        ("dq_stride_s", _i64),
+        ("dk", _ptr),
+        ("dk_stride_b", _i64),
+        ("dk_stride_s", _i64),
+        ("scale", _f32),
+    ]
+
+
 class DecodeParams(ctypes.Structure):
     _fields_ = [
         ("abi_version", _i32),
@@ -163,6 +194,7 @@ ENTRY_POINTS = {
     "atx_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnParams), _ptr]),
     "atx_attn_bwd": (ctypes.c_int, [ctypes.POINTER(AttnBwdParams), _ptr]),
     "atx_kq_masked_softmax_fwd": (ctypes.c_int, [ctypes.POINTER(KqParams), _ptr]),
+    "atx_kq_bwd": (ctypes.c_int, [ctypes.POINTER(KqBwdParams), _ptr]),
     "atx_attn_decode_fwd": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr]),
     "atx_last_error": (ctypes.c_char_p, []),
     "atx_abi_version": (ctypes.c_int, []),

@@ -196,6 +196,7 @@ __device__ inline u32x2 lds_ld8_tr16(const lds_t* p) {
         (__attribute__((address_space(3))) s16x4*)(p));
     return __builtin_bit_cast(u32x2, v);
 }
+__device__ inline u32x2 lds_ld8(const lds_t* p) { return *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(p); }
 __device__ inline void lds_st8(lds_t* p, u32x2 v) { *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(p) = v; }
 __device__ inline uint32_t lds_ld4(const lds_t* p) { return *reinterpret_cast<const __attribute__((address_space(3))) uint32_t*>(p); }
 __device__ inline void lds_st4(lds_t* p, uint32_t v) { *reinterpret_cast<__attribute__((address_space(3))) uint32_t*>(p) = v; }

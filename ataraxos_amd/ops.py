@@ -13,6 +13,8 @@ outside the kernels' range raises.
 * :func:`kq_policy` — the key-query policy head's logits, legal-move mask and
   softmax (``stratego/networks/move_net.py:92-95`` plus the callers' softmax,
   ``stratego/training/selfplay.py:284``).
+* :func:`kq_policy_backward` — its dq, dk for the gradient of the logits or
+  of the probabilities, in one launch.
 * :func:`attention_decode` — one query per (batch, head) against a KV cache.
 """
 
@@ -321,6 +323,81 @@ def kq_policy(
     p.scale = float(scale)
     _lib.check(_lib.call("atx_kq_masked_softmax_fwd", p, _stream(q)), "atx_kq_masked_softmax_fwd")
     return out
+
+
+def kq_policy_backward_supported(seq: int, dim: int, dtype: torch.dtype) -> bool:
+    """True when :func:`kq_policy_backward` covers this shape and dtype:
+    bf16/fp16, ``seq`` up to 128, ``dim`` a multiple of 16 up to 128."""
+    return dtype in _BWD_DTYPES and 1 <= seq <= 128 and dim % 16 == 0 and 16 <= dim <= 128
+
+
+def kq_policy_backward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    grad: torch.Tensor,
+    legal_move_mask: torch.Tensor | None = None,
+    scale: float | None = None,
+    output: str = "logits",
+    probs: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Gradients ``(dq, dk)`` of :func:`kq_policy` for the upstream gradient
+    ``grad`` (fp32 ``[B, S*S]``) of its ``output`` ("logits", or "probs" with
+    the forward's ``probs``).  Illegal entries pass no gradient.  One kernel
+    launch; returns contiguous tensors in q's dtype."""
+    _require_device("kq_policy_backward", q, k, grad)
+    if q.dim() != 3 or q.shape != k.shape:
+        raise ValueError(f"kq_policy_backward: q{tuple(q.shape)} and k{tuple(k.shape)} must both be [B, S, d]")
+    if q.dtype != k.dtype:
+        raise ValueError("kq_policy_backward: mixed dtypes")
+    if output not in ("probs", "logits"):
+        raise ValueError(f"kq_policy_backward: output must be 'probs' or 'logits', got {output!r}")
+    b, s, d = q.shape
+    if not kq_policy_backward_supported(s, d, q.dtype):
+        raise NotImplementedError(f"kq_policy_backward: {q.dtype}, seq {s}, dim {d} not covered by the kernel")
+    if tuple(grad.shape) != (b, s * s):
+        raise ValueError(f"kq_policy_backward: grad must be [{b}, {s * s}]")
+    grad = grad.float()
+    if grad.stride(1) != 1:
+        grad = grad.contiguous()
+    if output == "probs":
+        if probs is None or tuple(probs.shape) != (b, s * s):
+            raise ValueError("kq_policy_backward: output='probs' needs the forward's probs [B, S*S]")
+        _require_device("kq_policy_backward", q, probs)
+        probs = probs.float()
+        if probs.stride(1) != 1:
+            probs = probs.contiguous()
+    q, k = _aligned_rows(q), _aligned_rows(k)
+    mask = None
+    if legal_move_mask is not None:
+        if tuple(legal_move_mask.shape) != (b, s, s):
+            raise ValueError(f"kq_policy_backward: legal_move_mask must be [{b}, {s}, {s}]")
+        _require_device("kq_policy_backward", q, legal_move_mask)
+        mask = legal_move_mask if legal_move_mask.dtype == torch.bool else legal_move_mask != 0
+        if mask.stride(2) != 1:
+            mask = mask.contiguous()
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    dq = torch.empty((b, s, d), dtype=q.dtype, device=q.device)
+    dk = torch.empty((b, s, d), dtype=q.dtype, device=q.device)
+
+    p = _lib.KqBwdParams()
+    p.abi_version = _lib.ABI_VERSION
+    p.dtype = _DTYPES[q.dtype]
+    p.batch, p.seq, p.dim = b, s, d
+    p.out_mode = _lib.KQ_OUT_PROBS if output == "probs" else _lib.KQ_OUT_LOGITS
+    p.q, p.q_stride_b, p.q_stride_s = q.data_ptr(), q.stride(0), q.stride(1)
+    p.k, p.k_stride_b, p.k_stride_s = k.data_ptr(), k.stride(0), k.stride(1)
+    p.mask = mask.data_ptr() if mask is not None else None
+    p.mask_stride_b = mask.stride(0) if mask is not None else 0
+    p.mask_stride_s = mask.stride(1) if mask is not None else 0
+    p.grad, p.grad_stride_b = grad.data_ptr(), grad.stride(0)
+    p.probs = probs.data_ptr() if output == "probs" else None
+    p.probs_stride_b = probs.stride(0) if output == "probs" else 0
+    p.dq, p.dq_stride_b, p.dq_stride_s = dq.data_ptr(), dq.stride(0), dq.stride(1)
+    p.dk, p.dk_stride_b, p.dk_stride_s = dk.data_ptr(), dk.stride(0), dk.stride(1)
+    p.scale = float(scale)
+    _lib.check(_lib.call("atx_kq_bwd", p, _stream(q)), "atx_kq_bwd")
+    return dq, dk
 
 
 def attention_decode(

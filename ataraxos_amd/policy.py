@@ -9,6 +9,10 @@ returning the flattened ``(B, S*S)`` logits with illegal entries at -1e10.
 :meth:`KeyQueryPolicyHead.policy` additionally fuses the softmax that every
 caller applies to those logits (``stratego/training/selfplay.py:284``,
 ``stratego/training/move_trainer.py:118``) into the same kernel.
+
+Gradients (the Move trainer's ``loss.backward()``, move_trainer.py:140) of
+either output go through one HIP launch (:func:`ops.kq_policy_backward`) for
+bf16/fp16 q, k; fp32 inputs are differentiated with torch ops in fp32.
 """
 
 from __future__ import annotations
@@ -53,7 +57,10 @@ class _KqLogits(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g):  # type: ignore[override]
         q, k = ctx.saved_tensors
-        gq, gk = _logit_grads(g.float(), q, k, ctx.mask, ctx.scale)
+        if ops.kq_policy_backward_supported(q.shape[1], q.shape[2], q.dtype):
+            gq, gk = ops.kq_policy_backward(q, k, g, ctx.mask, ctx.scale, output="logits")
+        else:
+            gq, gk = _logit_grads(g.float(), q, k, ctx.mask, ctx.scale)
         return gq, gk, None, None
 
 
@@ -68,6 +75,9 @@ class _KqProbs(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g):  # type: ignore[override]
         q, k, probs = ctx.saved_tensors
+        if ops.kq_policy_backward_supported(q.shape[1], q.shape[2], q.dtype):
+            gq, gk = ops.kq_policy_backward(q, k, g, ctx.mask, ctx.scale, output="probs", probs=probs)
+            return gq, gk, None, None
         g = g.float()
         glogit = probs * (g - (g * probs).sum(dim=-1, keepdim=True))
         gq, gk = _logit_grads(glogit, q, k, ctx.mask, ctx.scale)

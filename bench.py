@@ -25,6 +25,7 @@ roofline = 18.2 M samples/s).  Also reported on the same line:
   (encoder self, decoder causal self, decoder cross with key padding);
 * ``decode``: the KV-cache decode kernel over config C5's 4 layers x 40 steps;
 * ``backward``: the attention backward kernel (dQ, dK, dV) of one C3 layer;
+* ``kq_backward``: the policy-head backward kernel (dq, dk) at config C2;
 * ``cpu_baseline``: the reference's math path (torch on the host CPU) on a
   bounded sample of the same layer, rank 0 only.
 
@@ -312,6 +313,28 @@ def time_backward(torch, ops, batch, dev, steps, warmup):
     return leg
 
 
+def time_kq_backward(torch, ops, batch, dev, steps, warmup):
+    """Backward of the C2 policy head (B=4096, 100x100, d=64, bf16 q/k): the
+    gradient the Move trainer takes through the logits, and through the
+    probabilities for a caller that differentiates those."""
+    g = torch.Generator(device=dev).manual_seed(49)
+    s, d = 100, 64
+    q = torch.randn(batch, s, d, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(batch, s, d, generator=g, device=dev).to(torch.bfloat16)
+    mask = torch.rand(batch, s, s, generator=g, device=dev) < 0.02
+    mask[:, 0, 0] |= ~mask.flatten(1).any(dim=1)
+    grad = torch.randn(batch, s * s, generator=g, device=dev)
+    probs = ops.kq_policy(q, k, mask, output="probs")
+    legs = {}
+    for output in ("logits", "probs"):
+        ms = _mean_launch_ms(
+            torch, lambda: ops.kq_policy_backward(q, k, grad, mask, output=output, probs=probs), steps, warmup)
+        # G (and P) fp32 + legality bytes + q, k read; dq, dk written
+        nbytes = batch * (s * s * 4 * (2 if output == "probs" else 1) + s * s + 4 * s * d * 2)
+        legs[output] = _leg(f"policy head backward, gradient of the {output}", ms, nbytes, batch)
+    return {"config": "C2 policy head backward, B=4096, 100x100, d=64, bf16 q/k, fp32 gradient", "legs": legs}
+
+
 def cpu_baseline(sample: int) -> dict:
     from oracle.cpu_baseline import attention_baseline
 
@@ -428,6 +451,7 @@ def main() -> int:
         result["belief_attention"] = time_belief(torch, ops, dev, args.steps, args.warmup)
         result["decode"] = time_decode(torch, ops, dev, max(3, args.steps // 10))
         result["backward"] = time_backward(torch, ops, batch, dev, args.steps, args.warmup)
+        result["kq_backward"] = time_kq_backward(torch, ops, batch, dev, args.steps, args.warmup)
         print("[bench] extras timed", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_sample)

@@ -196,6 +196,50 @@ typedef struct AtxKqParams {
  */
 int atx_kq_masked_softmax_fwd(const AtxKqParams* params, void* stream);
 
+/*
+ * Backward of the policy head: for every sample b, given the upstream
+ * gradient G = grad[b] (fp32, [seq * seq] from-major) with respect to the
+ * forward's output,
+ *   ATX_KQ_OUT_LOGITS: dL = G on legal entries, 0 on illegal ones;
+ *   ATX_KQ_OUT_PROBS:  dL = P * (G - sum(G * P)) on legal entries, 0 on
+ *                      illegal ones, with P = probs[b] the forward's output;
+ * then dq[b] = scale * dL k[b] and dk[b] = scale * dL^T q[b] (dL as
+ * [seq, seq]), written in q's dtype.  Masked entries get no gradient, as
+ * through masked_fill; a sample with no legal entry gets dq = dk = 0.
+ * 16-bit q / k only (ATX_DTYPE_BF16 or FP16), dim a multiple of 16 up to 128.
+ */
+typedef struct AtxKqBwdParams {
+    int32_t abi_version;
+    int32_t dtype;    /* of q, k, dq, dk: ATX_DTYPE_BF16 or FP16 */
+    int32_t batch;
+    int32_t seq;      /* 1..128 */
+    int32_t dim;      /* multiple of 16, <= 128 */
+    int32_t out_mode; /* ATX_KQ_OUT_*: what `grad` is the gradient of */
+    const void* q;
+    int64_t q_stride_b, q_stride_s;
+    const void* k;
+    int64_t k_stride_b, k_stride_s;
+    const uint8_t* mask; /* optional [batch, seq, seq]; nonzero = legal */
+    int64_t mask_stride_b, mask_stride_s;
+    const float* grad;   /* [batch, seq * seq], contiguous per sample */
+    int64_t grad_stride_b;
+    const float* probs;  /* ATX_KQ_OUT_PROBS: the forward's output; else NULL */
+    int64_t probs_stride_b;
+    void* dq;
+    int64_t dq_stride_b, dq_stride_s;
+    void* dk;
+    int64_t dk_stride_b, dk_stride_s;
+    float scale;
+} AtxKqBwdParams;
+
+/*
+ * Replaces the autograd backward through KeyQueryPolicyHead's product and
+ * mask (stratego/networks/move_net.py:92-95), and for ATX_KQ_OUT_PROBS the
+ * caller's softmax, that the Move trainer's loss.backward() runs
+ * (stratego/training/move_trainer.py:115-140).
+ */
+int atx_kq_bwd(const AtxKqBwdParams* params, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Single-query attention over a KV cache (incremental decode)              */
 /* ------------------------------------------------------------------------ */

@@ -39,3 +39,38 @@ def kq_probs(q: np.ndarray, k: np.ndarray, mask: np.ndarray | None, scale: float
     exists; with none, every entry is ``1/(S*S)``.
     """
     return softmax_lastdim(kq_logits(q, k, mask, scale))
+
+
+def kq_backward(
+    q: np.ndarray,
+    k: np.ndarray,
+    mask: np.ndarray | None,
+    scale: float,
+    grad: np.ndarray,
+    wrt: str = "logits",
+) -> tuple[np.ndarray, np.ndarray]:
+    """Gradients ``(dq, dk)`` of the policy head for an upstream ``grad``
+    ``[B, S*S]`` with respect to :func:`kq_logits` (``wrt="logits"``, what the
+    Move trainer's loss back-propagates into, stratego/training/move_trainer.py:115-140)
+    or to :func:`kq_probs` (``wrt="probs"``), in float64.
+
+    By the chain rule through move_net.py:92-95: the softmax over all ``S*S``
+    entries gives ``dL = P * (G - sum(G * P))``; ``masked_fill`` passes no
+    gradient to illegal entries (``dL = 0`` there, also in a sample with no
+    legal entry, whose P is uniform); ``L = scale * q k^T`` gives
+    ``dq = scale * dL k`` and ``dk = scale * dL^T q`` with ``dL`` as
+    ``[B, S, S]`` from-major.
+    """
+    q64 = np.asarray(q, dtype=np.float64)
+    k64 = np.asarray(k, dtype=np.float64)
+    b, s, _ = q64.shape
+    g = np.asarray(grad, dtype=np.float64).reshape(b, s * s)
+    if wrt == "probs":
+        p = kq_probs(q64, k64, mask, scale)
+        g = p * (g - np.sum(g * p, axis=-1, keepdims=True))
+    elif wrt != "logits":
+        raise ValueError(f"wrt must be 'logits' or 'probs', got {wrt!r}")
+    g = g.reshape(b, s, s)
+    if mask is not None:
+        g = np.where(np.asarray(mask, dtype=bool), g, 0.0)
+    return np.matmul(g, k64) * scale, np.matmul(g.swapaxes(-1, -2), q64) * scale

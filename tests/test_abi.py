@@ -27,6 +27,7 @@ STRUCTS = {
     "AtxAttnParams": _lib.AttnParams,
     "AtxAttnBwdParams": _lib.AttnBwdParams,
     "AtxKqParams": _lib.KqParams,
+    "AtxKqBwdParams": _lib.KqBwdParams,
     "AtxDecodeParams": _lib.DecodeParams,
 }
 
@@ -206,6 +207,35 @@ def test_policy_validation_codes():
         saved = getattr(p, field)
         setattr(p, field, value)
         _expect("atx_kq_masked_softmax_fwd", p, code, text)
+        setattr(p, field, saved)
+
+
+def test_policy_backward_validation_codes():
+    p = _lib.KqBwdParams()
+    p.abi_version, p.dtype, p.batch, p.seq, p.dim = _lib.ABI_VERSION, _lib.DTYPE_BF16, 4, 100, 64
+    p.out_mode = _lib.KQ_OUT_LOGITS
+    p.q = p.k = p.dq = p.dk = p.grad = 1 << 20  # never dereferenced: every case fails validation
+    p.q_stride_b = p.k_stride_b = p.dq_stride_b = p.dk_stride_b = 6400
+    p.q_stride_s = p.k_stride_s = p.dq_stride_s = p.dk_stride_s = 64
+    p.grad_stride_b = 10000
+    p.scale = 0.125
+    assert _lib.load().atx_kq_bwd(None, None) == _lib.ERR_INVALID_ARGUMENT
+    for field, value, code, text in [
+        ("abi_version", 3, _lib.ERR_ABI, "abi_version"),
+        ("dtype", _lib.DTYPE_FP32, _lib.ERR_UNSUPPORTED, "fp32"),
+        ("out_mode", 5, _lib.ERR_INVALID_ARGUMENT, "out_mode"),
+        ("out_mode", _lib.KQ_OUT_PROBS, _lib.ERR_INVALID_ARGUMENT, "null"),  # probs mode needs probs
+        ("seq", 129, _lib.ERR_UNSUPPORTED, "seq"),
+        ("dim", 40, _lib.ERR_UNSUPPORTED, "dim"),
+        ("scale", 0.0, _lib.ERR_INVALID_ARGUMENT, "scale"),
+        ("grad_stride_b", 9999, _lib.ERR_INVALID_ARGUMENT, "stride"),
+        ("dq_stride_s", 32, _lib.ERR_INVALID_ARGUMENT, "overlap"),
+        ("k_stride_s", 68, _lib.ERR_INVALID_ARGUMENT, "16-byte"),
+        ("q_stride_s", -64, _lib.ERR_UNSUPPORTED, ">= 0"),
+    ]:
+        saved = getattr(p, field)
+        setattr(p, field, value)
+        _expect("atx_kq_bwd", p, code, text)
         setattr(p, field, saved)
 
 

@@ -1,0 +1,186 @@
+"""Parity of the policy-head backward (``atx_kq_bwd``) against the float64
+oracle's gradients (``oracle.policy.kq_backward``).
+
+Inputs are drawn on the CPU from seeded generators; q, k are rounded to the
+kernel's 16-bit dtype first, and the oracle runs in float64 on the same
+values.  In probs mode the kernel is given the HIP forward's probabilities.
+
+Tolerance (gradients scale with the upstream gradient, so it is relative to
+each gradient's own size): ``max|g - ref| <= 2e-2 * max|ref|`` and
+``||g - ref||_F <= 1e-2 * ||ref||_F``; where the exact gradient vanishes,
+``max|ref|`` is floored at 1e-4.  A sample with no legal entry must get
+exactly 0.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from ataraxos_amd import KeyQueryPolicyHead, masked_policy_logits, masked_policy_softmax, ops
+from oracle.policy import kq_backward
+from tests._cases import legal_mask, randn, to_np64
+
+pytestmark = pytest.mark.gpu
+
+REL_MAX = 2e-2
+REL_FRO = 1e-2
+ZERO_FLOOR = 1e-4
+
+
+def _announce(msg: str) -> None:
+    print(f"\n[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def assert_grad_close(got: torch.Tensor, ref: np.ndarray, what: str) -> None:
+    g = to_np64(got)
+    assert g.shape == ref.shape, f"{what}: shape {g.shape} vs {ref.shape}"
+    assert np.isfinite(g).all(), f"{what}: non-finite values"
+    scale = max(float(np.max(np.abs(ref))), ZERO_FLOOR)
+    err = float(np.max(np.abs(g - ref)))
+    assert err <= REL_MAX * scale, f"{what}: max-abs {err:.3e} > {REL_MAX} * {scale:.3e}"
+    if scale > ZERO_FLOOR:
+        fro = float(np.linalg.norm(g - ref) / np.linalg.norm(ref))
+        assert fro <= REL_FRO, f"{what}: relative Frobenius error {fro:.3e} > {REL_FRO}"
+
+
+def run_case(cuda, b, s, d, dtype, output, p_legal=0.02, seed=0, scale=None, empty_sample=False, mask_view=False):
+    _announce(f"kq bwd b={b} s={s} d={d} {dtype} {output} p={p_legal} empty={empty_sample} view={mask_view}")
+    q = randn((b, s, d), seed, dtype)
+    k = randn((b, s, d), seed + 1, dtype)
+    mask = None if p_legal is None else legal_mask(b, s, seed + 2, p_legal)
+    if mask is not None and empty_sample:
+        mask[b // 2] = False
+    grad = randn((b, s * s), seed + 3, torch.float32)
+    sc = scale if scale is not None else d**-0.5
+    qd, kd, gd = q.to(cuda), k.to(cuda), grad.to(cuda)
+    md = None
+    if mask is not None:
+        if mask_view:  # rows of a wider buffer: row stride s + 3, not a multiple of 4
+            big = torch.zeros(b, s, s + 3, dtype=torch.bool)
+            big[:, :, :s] = mask
+            md = big.to(cuda)[:, :, :s]
+        else:
+            md = mask.to(cuda)
+    probs = ops.kq_policy(qd, kd, md, scale=sc, output="probs") if output == "probs" else None
+    dq, dk = ops.kq_policy_backward(qd, kd, gd, md, sc, output=output, probs=probs)
+    torch.cuda.synchronize()
+    ref = kq_backward(to_np64(q), to_np64(k), None if mask is None else mask.numpy(), sc, grad.numpy().astype(np.float64),
+                      wrt=output)
+    assert_grad_close(dq, ref[0], f"dq b={b} s={s} d={d} {output}")
+    assert_grad_close(dk, ref[1], f"dk b={b} s={s} d={d} {output}")
+    if empty_sample:
+        assert (dq[b // 2] == 0).all() and (dk[b // 2] == 0).all()
+
+
+@pytest.mark.parametrize("output", ["logits", "probs"])
+def test_config2_shape(cuda, output):
+    """C2 (S=100, d=64, Bernoulli(0.02) legal moves, bf16) at B=256."""
+    run_case(cuda, 256, 100, 64, torch.bfloat16, output, seed=10)
+
+
+@pytest.mark.parametrize("output", ["logits", "probs"])
+def test_config2_full_batch_against_torch_fp32(cuda, output):
+    """C2 at B=4096 against torch fp32 autograd of the reference head's ops
+    (matmul, masked_fill(-1e10), softmax) on the GPU; bitwise repeatable."""
+    _announce(f"kq bwd C2 full batch {output}")
+    b, s, d = 4096, 100, 64
+    q, k = randn((b, s, d), 20, torch.bfloat16).to(cuda), randn((b, s, d), 21, torch.bfloat16).to(cuda)
+    mask = legal_mask(b, s, 22).to(cuda)
+    g = randn((b, s * s), 23, torch.float32).to(cuda)
+    probs = ops.kq_policy(q, k, mask, scale=0.125, output="probs") if output == "probs" else None
+    got = ops.kq_policy_backward(q, k, g, mask, 0.125, output=output, probs=probs)
+    again = ops.kq_policy_backward(q, k, g, mask, 0.125, output=output, probs=probs)
+    torch.cuda.synchronize()
+    assert torch.equal(got[0], again[0]) and torch.equal(got[1], again[1])
+    qf, kf = q.float().requires_grad_(True), k.float().requires_grad_(True)
+    logits = (torch.matmul(qf, kf.transpose(1, 2).contiguous()) * 0.125).masked_fill(~mask, -1e10).reshape(b, -1)
+    out = torch.softmax(logits, dim=-1) if output == "probs" else logits
+    want = torch.autograd.grad(out, (qf, kf), g)
+    for name, a, w in zip(("dq", "dk"), got, want):
+        scale = w.abs().max().item()
+        err = (a.float() - w).abs().max().item()
+        assert err <= REL_MAX * scale, f"{name}: {err:.3e} > {REL_MAX} * {scale:.3e}"
+        assert ((a.float() - w).norm() / w.norm()).item() <= REL_FRO
+
+
+@pytest.mark.parametrize("s", [1, 5, 17, 32, 33, 64, 65, 99, 100, 128])
+@pytest.mark.parametrize("output", ["logits", "probs"])
+def test_seq_lengths(cuda, s, output):
+    run_case(cuda, 8, s, 64, torch.bfloat16, output, p_legal=0.3, seed=30 + s)
+
+
+@pytest.mark.parametrize("d", [16, 32, 48, 64, 80, 96, 112, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_dims(cuda, d, dtype):
+    run_case(cuda, 8, 100, d, dtype, "logits", p_legal=0.1, seed=50 + d)
+
+
+@pytest.mark.parametrize("output", ["logits", "probs"])
+def test_no_mask(cuda, output):
+    run_case(cuda, 8, 100, 64, torch.bfloat16, output, p_legal=None, seed=60)
+
+
+@pytest.mark.parametrize("output", ["logits", "probs"])
+def test_sample_without_legal_moves_gets_zero(cuda, output):
+    run_case(cuda, 8, 100, 64, torch.bfloat16, output, seed=61, empty_sample=True)
+
+
+@pytest.mark.parametrize("s", [17, 100])
+def test_mask_rows_of_a_wider_buffer(cuda, s):
+    """Mask rows not 4-byte aligned: the byte-wise legality path."""
+    run_case(cuda, 8, s, 64, torch.bfloat16, "probs", p_legal=0.3, seed=62, mask_view=True)
+
+
+def test_autograd_takes_the_hip_backward(cuda):
+    """masked_policy_logits / masked_policy_softmax under autograd return
+    exactly the kernel's gradients."""
+    _announce("kq bwd autograd")
+    b, s, d = 16, 100, 64
+    q, k = randn((b, s, d), 70, torch.bfloat16).to(cuda), randn((b, s, d), 71, torch.bfloat16).to(cuda)
+    mask = legal_mask(b, s, 72).to(cuda)
+    g = randn((b, s * s), 73, torch.float32).to(cuda)
+    for fn, output in ((masked_policy_logits, "logits"), (masked_policy_softmax, "probs")):
+        qa, ka = q.clone().requires_grad_(True), k.clone().requires_grad_(True)
+        out = fn(qa, ka, mask, 0.125)
+        got = torch.autograd.grad(out, (qa, ka), g)
+        probs = out.detach() if output == "probs" else None
+        want = ops.kq_policy_backward(q, k, g, mask, 0.125, output=output, probs=probs)
+        for a, w in zip(got, want):
+            assert torch.equal(a, w)
+
+
+def test_policy_head_module_gradients(cuda):
+    """KeyQueryPolicyHead in bf16 on the GPU: input gradient through the
+    projections and the HIP forward/backward agrees with float64 autograd of
+    the head's math on the same parameters."""
+    _announce("kq bwd module")
+    torch.manual_seed(3)
+    head = KeyQueryPolicyHead(128, 64).to(cuda, torch.bfloat16)
+    x = randn((8, 100, 128), 80, torch.bfloat16).to(cuda).requires_grad_(True)
+    mask = legal_mask(8, 100, 81, 0.1).to(cuda)
+    g = randn((8, 100 * 100), 82, torch.float32).to(cuda)
+    out = head(x, mask)
+    (gx,) = torch.autograd.grad(out.float(), (x,), g)
+    h64 = KeyQueryPolicyHead(128, 64).double()
+    h64.load_state_dict({n: t.double().cpu() for n, t in head.state_dict().items()})
+    x64 = x.detach().double().cpu().requires_grad_(True)
+    (want,) = torch.autograd.grad(h64(x64, mask.cpu()), (x64,), g.double().cpu())
+    err = (gx.double().cpu() - want).abs().max().item()
+    assert err <= REL_MAX * want.abs().max().item(), err
+
+
+def test_fp32_and_unsupported_dims_fall_back(cuda):
+    q = torch.randn(4, 100, 64, device=cuda)
+    with pytest.raises(NotImplementedError):
+        ops.kq_policy_backward(q, q, torch.zeros(4, 10000, device=cuda))
+    qb = torch.randn(4, 100, 40, device=cuda, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        ops.kq_policy_backward(qb, qb, torch.zeros(4, 10000, device=cuda))
+    qa = q.clone().requires_grad_(True)
+    masked_policy_logits(qa, q, None).sum().backward()
+    assert torch.isfinite(qa.grad).all()

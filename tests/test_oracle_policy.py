@@ -113,3 +113,64 @@ def test_decode_first_step_returns_value():
     v = rnd(2, 4, 1, 16, seed=5)
     out = decode_step(rnd(2, 4, 16, seed=6), rnd(2, 4, 1, 16, seed=7), v)
     np.testing.assert_allclose(out, v[:, :, 0], atol=1e-15)
+
+
+# --- backward -----------------------------------------------------------------
+
+
+def _torch_policy_grads(q, k, mask, scale, grad, wrt):
+    """dq, dk by torch autograd (float64, CPU) through matmul, masked_fill(-1e10)
+    and (``wrt="probs"``) softmax: the reference head's operations."""
+    tq, tk = (torch.from_numpy(np.ascontiguousarray(x)).requires_grad_(True) for x in (q, k))
+    logits = torch.matmul(tq, tk.transpose(-2, -1)) * scale
+    if mask is not None:
+        logits = logits.masked_fill(~torch.from_numpy(mask), ILLEGAL_LOGIT)
+    out = logits.reshape(q.shape[0], -1)
+    if wrt == "probs":
+        out = torch.softmax(out, dim=-1)
+    out.backward(torch.from_numpy(np.ascontiguousarray(grad)))
+    return tq.grad.numpy(), tk.grad.numpy()
+
+
+@pytest.mark.parametrize("wrt", ["logits", "probs"])
+@pytest.mark.parametrize("masked", [False, True])
+def test_backward_matches_torch_autograd(wrt, masked):
+    from oracle.policy import kq_backward
+
+    b, s, d = 3, 17, 16
+    q, k = rnd(b, s, d, seed=1), rnd(b, s, d, seed=2)
+    mask = mask_of(b, s, 0.2, seed=3) if masked else None
+    if masked:
+        mask[2] = False  # a sample with no legal move: uniform P, zero gradient
+    g = rnd(b, s * s, seed=4)
+    got = kq_backward(q, k, mask, 0.25, g, wrt=wrt)
+    want = _torch_policy_grads(q, k, mask, 0.25, g, wrt)
+    for a, w in zip(got, want):
+        np.testing.assert_allclose(a, w, rtol=1e-10, atol=1e-12)
+    if masked:
+        assert np.all(got[0][2] == 0) and np.all(got[1][2] == 0)
+
+
+@pytest.mark.parametrize("wrt", ["logits", "probs"])
+def test_backward_central_finite_differences(wrt):
+    """Each entry of dq, dk equals d<f(q, k), G>/dx by central differences of
+    the (independently pinned) forward f = kq_logits or kq_probs."""
+    from oracle.policy import kq_backward
+
+    b, s, d, scale = 1, 4, 3, 0.7
+    q, k = rnd(b, s, d, seed=5), rnd(b, s, d, seed=6)
+    mask = mask_of(b, s, 0.5, seed=7)
+    g = rnd(b, s * s, seed=8)
+    f = kq_probs if wrt == "probs" else kq_logits
+    grads = kq_backward(q, k, mask, scale, g, wrt=wrt)
+    eps = 1e-6
+    for which, gr in enumerate(grads):
+        fd = np.zeros_like(gr)
+        for idx in np.ndindex(*gr.shape):
+            xs_p, xs_m = [q.copy(), k.copy()], [q.copy(), k.copy()]
+            xs_p[which][idx] += eps
+            xs_m[which][idx] -= eps
+            fp = np.sum(np.where(f(*xs_p, mask, scale) > -1e9, f(*xs_p, mask, scale), 0.0) * g)
+            fm = np.sum(np.where(f(*xs_m, mask, scale) > -1e9, f(*xs_m, mask, scale), 0.0) * g)
+            fd[idx] = (fp - fm) / (2 * eps)
+        np.testing.assert_allclose(gr, fd, rtol=1e-6, atol=1e-8)
