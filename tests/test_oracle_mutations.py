@@ -174,3 +174,29 @@ def test_backward_gqa_mistake_is_caught_by_torch_autograd():
     np.testing.assert_allclose(dv, ref[1], rtol=1e-10, atol=1e-12)
     _, mk, mv = mutant_bwd_gqa_first_head(q, k, v, d_o)
     assert not np.allclose(mk, ref[0], atol=1e-6) and not np.allclose(mv, ref[1], atol=1e-6)
+
+
+def test_policy_backward_mistakes_are_caught_by_torch_autograd():
+    """Policy-head gradient mutants: the softmax term dropped (dL = P * G) and
+    the mask not applied to the gradient.  torch autograd through the
+    reference head's operations rejects both."""
+    from oracle.policy import ILLEGAL_LOGIT, kq_backward
+
+    b, s, d, scale = 2, 9, 8, 0.35
+    q, k, g = rnd(b, s, d, seed=1), rnd(b, s, d, seed=2), rnd(b, s * s, seed=3)
+    mask = np.random.default_rng(4).random((b, s, s)) < 0.4
+    mask[:, 0, 0] = True
+    tq, tk = (torch.from_numpy(x).requires_grad_(True) for x in (q, k))
+    logits = (torch.matmul(tq, tk.transpose(1, 2)) * scale).masked_fill(~torch.from_numpy(mask), ILLEGAL_LOGIT)
+    torch.softmax(logits.reshape(b, -1), dim=-1).backward(torch.from_numpy(g))
+    ref = tq.grad.numpy()
+    np.testing.assert_allclose(kq_backward(q, k, mask, scale, g, wrt="probs")[0], ref, rtol=1e-10, atol=1e-12)
+    p = kq_probs(q, k, mask, scale)
+    dl = np.where(mask, (p * g).reshape(b, s, s), 0.0)  # mutant: no "- sum(G * P)"
+    assert not np.allclose(dl @ k * scale, ref, atol=1e-6)
+    tq2 = torch.from_numpy(q).requires_grad_(True)
+    logits2 = (torch.matmul(tq2, torch.from_numpy(k).transpose(1, 2)) * scale).masked_fill(~torch.from_numpy(mask), ILLEGAL_LOGIT)
+    logits2.reshape(b, -1).backward(torch.from_numpy(g))
+    unmasked = g.reshape(b, s, s) @ k * scale  # mutant: gradient reaches illegal entries
+    np.testing.assert_allclose(kq_backward(q, k, mask, scale, g)[0], tq2.grad.numpy(), rtol=1e-10, atol=1e-12)
+    assert not np.allclose(unmasked, tq2.grad.numpy(), atol=1e-6)
