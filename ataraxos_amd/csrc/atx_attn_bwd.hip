@@ -21,9 +21,10 @@
 //    fed from registers.
 // Every output tile has one owner: no atomics, no cross-wave reductions, and
 // the result does not depend on timing.
-// Masked scores get dS = 0 exactly (the gradient of masked_fill); a query
-// that sees no key has P = NaN, so its dO reaches dV as NaN, as autograd
-// through the reference's math gives.
+// Masked scores get dS = 0 (the gradient of masked_fill); a query that sees
+// no key has P = NaN, so its dO reaches dV as NaN, as autograd through the
+// reference's math gives.  Key tiles that are fully usable (or unusable) for
+// a whole wave skip the per-score masking (or the whole tile).
 #include "ataraxos_attn.h"
 #include "atx_common.hpp"
 
@@ -74,14 +75,6 @@ __device__ inline int quad_off(int r, int e) {
     return chunk_off<D>(r, e >> 3) + (e & 7) * 2;
 }
 
-// x where bit `bit` of `bits` is set, else +0 (a mask, not a compare: the
-// bit index is a compile-time constant after unrolling).
-__device__ inline float keep_bit(float x, uint64_t bits, int bit) {
-    const uint32_t w = bit < 32 ? (uint32_t)bits : (uint32_t)(bits >> 32);
-    const uint32_t m = (uint32_t)((int32_t)(w << (31 - (bit & 31))) >> 31);
-    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) & m);
-}
-
 }  // namespace
 
 // Bytes of LDS for one workgroup: K, V (rk rows), Q, dO (rq rows), and the
@@ -122,7 +115,7 @@ void attn_bwd_16bit(BwdArgs a) {
     lds_t* const sq = sv + RK * RS;
     lds_t* const sdo = sq + RQ * RS;
     lds_t* const slse = sdo + RQ * RS;    // RQ floats: log-sum-exp in log2 units
-    lds_t* const sdelta = slse + RQ * 4;  // RQ floats: rowsum(O * dO)
+    lds_t* const sdelta = slse + RQ * 4;  // RQ floats: -rowsum(O * dO)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -157,15 +150,45 @@ void attn_bwd_16bit(BwdArgs a) {
     if (wave < nqt) load_o(wave);
 
     // ---- stage K, V (RK rows), Q, dO (RQ rows) ------------------------------
-    for (int idx = tid; idx < RK * CH; idx += kThreads) {
-        const int r = idx / CH, c = idx - (idx / CH) * CH;
-        lds_st16(sk + chunk_off<D>(r, c), buf_ld16(rk, (uint32_t)(r * a.kss + c * 8) * 2));
-        lds_st16(sv + chunk_off<D>(r, c), buf_ld16(rv, (uint32_t)(r * a.vss + c * 8) * 2));
-    }
-    for (int idx = tid; idx < RQ * CH; idx += kThreads) {
-        const int r = idx / CH, c = idx - (idx / CH) * CH;
-        lds_st16(sq + chunk_off<D>(r, c), buf_ld16(rq, (uint32_t)(r * a.qss + c * 8) * 2));
-        lds_st16(sdo + chunk_off<D>(r, c), buf_ld16(rdo, (uint32_t)(r * a.doss + c * 8) * 2));
+    // Every load of a batch is issued before the first LDS store, so a
+    // thread waits for memory once per batch (once in all at C3), not once
+    // per row chunk.  Batches cover RK rows of all four tensors; query rows
+    // past RK (S_q > S_kv) follow in a loop of their own.
+    {
+        constexpr int KIT = (RK * CH + kThreads - 1) / kThreads;
+        constexpr int UB = KIT < 4 ? KIT : 4;  // chunks per thread per batch
+        const int nq = RQ * CH;
+        for (int base = 0; base < RK * CH; base += UB * kThreads) {
+            u32x4 kx[UB], vx[UB], qx[UB], dx[UB];
+#pragma unroll
+            for (int u = 0; u < UB; ++u) {
+                const int idx = base + u * kThreads + tid;
+                const int r = idx / CH, c = idx - (idx / CH) * CH;
+                const bool kin = idx < RK * CH, qin = idx < nq;
+                kx[u] = buf_ld16(rk, kin ? (uint32_t)(r * a.kss + c * 8) * 2 : kOut);
+                vx[u] = buf_ld16(rv, kin ? (uint32_t)(r * a.vss + c * 8) * 2 : kOut);
+                qx[u] = buf_ld16(rq, qin ? (uint32_t)(r * a.qss + c * 8) * 2 : kOut);
+                dx[u] = buf_ld16(rdo, qin ? (uint32_t)(r * a.doss + c * 8) * 2 : kOut);
+            }
+#pragma unroll
+            for (int u = 0; u < UB; ++u) {
+                const int idx = base + u * kThreads + tid;
+                const int r = idx / CH, c = idx - (idx / CH) * CH;
+                if (idx < RK * CH) {
+                    lds_st16(sk + chunk_off<D>(r, c), kx[u]);
+                    lds_st16(sv + chunk_off<D>(r, c), vx[u]);
+                }
+                if (idx < nq) {
+                    lds_st16(sq + chunk_off<D>(r, c), qx[u]);
+                    lds_st16(sdo + chunk_off<D>(r, c), dx[u]);
+                }
+            }
+        }
+        for (int idx = RK * CH + tid; idx < nq; idx += kThreads) {
+            const int r = idx / CH, c = idx - (idx / CH) * CH;
+            lds_st16(sq + chunk_off<D>(r, c), buf_ld16(rq, (uint32_t)(r * a.qss + c * 8) * 2));
+            lds_st16(sdo + chunk_off<D>(r, c), buf_ld16(rdo, (uint32_t)(r * a.doss + c * 8) * 2));
+        }
     }
     // Rows of the last pair that no query tile covers: defined lse and delta.
     for (int r = nqt * 16 + tid; r < RQ; r += kThreads) {
@@ -175,12 +198,19 @@ void attn_bwd_16bit(BwdArgs a) {
 
     // Usable keys of this lane in phase 1 (bit 4*kt + i <-> key 16*kt + 4g + i).
     uint64_t kbits = 0;
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt) {
+        const int n = min(max(a.Skv - (kt * 16 + 4 * g), 0), 4);
+        kbits |= (uint64_t)((1u << n) - 1u) << (4 * kt);
+    }
     const uint8_t* prow = a.kpad ? a.kpad + (int64_t)b * a.kpsb : nullptr;
-    for (int kt = 0; kt < NKT; ++kt)
-        for (int i = 0; i < 4; ++i) {
-            const int key = kt * 16 + 4 * g + i;
-            if (key < a.Skv && !(prow && prow[key])) kbits |= (uint64_t)1 << (4 * kt + i);
-        }
+    if (prow) {
+        for (int kt = 0; kt < NKT; ++kt)
+            for (int i = 0; i < 4; ++i) {
+                const int key = kt * 16 + 4 * g + i;
+                if (key < a.Skv && prow[key]) kbits &= ~((uint64_t)1 << (4 * kt + i));
+            }
+    }
     __syncthreads();
 
     // Per-lane LDS offsets.  Operand reads of 16-row tiles: row m, chunks
@@ -218,10 +248,7 @@ void attn_bwd_16bit(BwdArgs a) {
     };
     auto dot8 = [&](u32x4 x, u32x4 y, float acc) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            acc = __builtin_fmaf(M::to_float((uint16_t)(x[j] & 0xffffu)), M::to_float((uint16_t)(y[j] & 0xffffu)), acc);
-            acc = __builtin_fmaf(M::to_float((uint16_t)(x[j] >> 16)), M::to_float((uint16_t)(y[j] >> 16)), acc);
-        }
+        for (int j = 0; j < 4; ++j) acc = M::dot2(x[j], y[j], acc);
         return acc;
     };
 
@@ -254,37 +281,63 @@ void attn_bwd_16bit(BwdArgs a) {
             }
             ok &= cb;
         }
-        // S^T = K Q^T, masked, in log2 units
-        f32x4 s[NKT];
+        // Keys at or past kend are unusable for every query of the tile;
+        // tiles below kfull need no per-score mask (no padding, every key
+        // < S_kv and, causal, <= the tile's first query).
+        const int kend = a.causal ? min(a.Skv, qt * 16 + 16) : a.Skv;
+        const int kfull = prow ? 0 : (a.causal ? min(a.Skv, qt * 16 + 1) : a.Skv);
+        // S^T = K Q^T (raw scores; masked ones -inf)
+        f32x4 s[NKT];  // tiles at or past kend are never read
         float mx = kNegInf;
 #pragma unroll
         for (int kt = 0; kt < NKT; ++kt) {
-            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (kt * 16 < kend) {
+                f32x4 acc = M::mma(ld_op(sk + kt * 16 * RS, 0), qop[0], f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-            for (int i = 0; i < NI; ++i) acc = M::mma(ld_op(sk + kt * 16 * RS, i), qop[i], acc);
+                for (int i = 1; i < NI; ++i) acc = M::mma(ld_op(sk + kt * 16 * RS, i), qop[i], acc);
+                if (kt * 16 + 16 > kfull) {
+                    // keep or -inf by bit masks (whole-vector casts: a bit
+                    // cast of one vector element reads element 0)
+                    const uint32_t w = (uint32_t)(ok >> (4 * kt));
+                    u32x4 ab = __builtin_bit_cast(u32x4, acc);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc[i] = ((ok >> (4 * kt + i)) & 1) ? acc[i] * a.c2 : kNegInf;
-                mx = fmaxf(mx, acc[i]);
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t keep = (uint32_t)((int32_t)(w << (31 - i)) >> 31);
+                        ab[i] = (ab[i] & keep) | (~keep & 0xff800000u);
+                    }
+                    acc = __builtin_bit_cast(f32x4, ab);
+                }
+                mx = fmaxf(fmaxf(mx, acc[0]), acc[1]);
+                mx = fmaxf(fmaxf(mx, acc[2]), acc[3]);
+                s[kt] = acc;
             }
-            s[kt] = acc;
         }
         mx = colgroup_max(mx);
-        const float base = mx == kNegInf ? 0.f : mx;
+        // no usable key: P = 0 everywhere here (dQ = 0); lse stays -inf
+        const bool empty = mx == kNegInf;
+        const float nbase = empty ? 0.f : -mx * a.c2;
         float sum = 0.f;
 #pragma unroll
-        for (int kt = 0; kt < NKT; ++kt)
+        for (int kt = 0; kt < NKT; ++kt) {
+            if (kt * 16 < kend) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sum += fast_exp2(s[kt][i] - base);
+                for (int i = 0; i < 4; ++i) {
+                    s[kt][i] = fast_exp2(__builtin_fmaf(s[kt][i], a.c2, nbase));  // unnormalised P
+                    sum += s[kt][i];
+                }
+            }
+        }
         sum = colgroup_sum(sum);
-        // no usable key: P = 0 everywhere here (dQ = 0); lse stays -inf
-        const float lse = mx == kNegInf ? kNegInf : base + __builtin_log2f(sum);
-        const float lsub = mx == kNegInf ? 0.f : lse;
+        const float lse = empty ? kNegInf : mx * a.c2 + __builtin_log2f(sum);
+        const float rs = empty ? 0.f : a.scale / sum;  // normalisation and dQ's scale
+        const float ndelta = empty ? 0.f : -delta;
         if (g == 0) {
             lds_st4(slse + qrow * 4, __builtin_bit_cast(uint32_t, lse));
-            lds_st4(sdelta + qrow * 4, __builtin_bit_cast(uint32_t, delta));
+            lds_st4(sdelta + qrow * 4, __builtin_bit_cast(uint32_t, ndelta));
         }
-        // dP^T = V dO^T, dS^T = P^T (dP^T - delta), packed per 32-key chunk
+        const f32x4 ndelta4 = f32x4{ndelta, ndelta, ndelta, ndelta};
+        // dP^T - delta = V dO^T - delta (the accumulator starts at -delta),
+        // scale * dS^T = P^T (dP^T - delta) * scale, packed per 32-key chunk
         u32x4 dsk[NKC];
 #pragma unroll
         for (int c = 0; c < NKC; ++c) {
@@ -292,36 +345,44 @@ void attn_bwd_16bit(BwdArgs a) {
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 const int kt = 2 * c + hh;
-                f32x4 dp = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (kt * 16 < kend) {
+                    f32x4 dp = M::mma(ld_op(sv + kt * 16 * RS, 0), doop[0], ndelta4);
 #pragma unroll
-                for (int i = 0; i < NI; ++i) dp = M::mma(ld_op(sv + kt * 16 * RS, i), doop[i], dp);
+                    for (int i = 1; i < NI; ++i) dp = M::mma(ld_op(sv + kt * 16 * RS, i), doop[i], dp);
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    ds[4 * hh + i] = keep_bit(fast_exp2(s[kt][i] - lsub) * (dp[i] - delta), ok, 4 * kt + i);
+                    for (int i = 0; i < 4; ++i) ds[4 * hh + i] = s[kt][i] * (rs * dp[i]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) ds[4 * hh + i] = 0.f;
+                }
             }
             dsk[c] = u32x4{M::pack2(ds[0], ds[1]), M::pack2(ds[2], ds[3]), M::pack2(ds[4], ds[5]), M::pack2(ds[6], ds[7])};
         }
-        // dQ^T = K^T dS^T
+        // dQ^T = K^T (scale * dS^T)
         f32x4 dq[NDT];
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int dt = 0; dt < NDT; ++dt) dq[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < NKC; ++c) {
-                const u32x2 lo = lds_ld8_tr16(sk + 32 * c * RS + troff[dt]);
-                const u32x2 hi = lds_ld8_tr16(sk + (32 * c + 16) * RS + troff[dt]);
-                acc = M::mma(u32x4{lo[0], lo[1], hi[0], hi[1]}, dsk[c], acc);
+        for (int c = 0; c < NKC; ++c) {
+            if (c * 32 < kend) {
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    const u32x2 lo = lds_ld8_tr16(sk + 32 * c * RS + troff[dt]);
+                    const u32x2 hi = lds_ld8_tr16(sk + (32 * c + 16) * RS + troff[dt]);
+                    dq[dt] = M::mma(u32x4{lo[0], lo[1], hi[0], hi[1]}, dsk[c], dq[dt]);
+                }
             }
-            dq[dt] = acc;
         }
-        store_row(rdq, a.dqss, qrow, dq, a.scale);
+        store_row(rdq, a.dqss, qrow, dq, 1.0f);
     }
     __syncthreads();  // log-sum-exp and delta of every query are in LDS
 
     // ---- phase 2: one 16-key tile per wave pass ----------------------------
     for (int kt = wave; kt < NKT; kt += kWaves) {
+        if (kt * 16 >= a.Skv) break;  // no key here: nothing to compute or store
         const int key = kt * 16 + m;
         const bool kok = key < a.Skv && !(prow && prow[key]);
+        const bool kfull = __builtin_amdgcn_ballot_w64(!kok) == 0;
         const lds_t* const kbase = sk + kt * 16 * RS;
         const lds_t* const vbase = sv + kt * 16 * RS;
         u32x4 kop[NI], vop[NI];
@@ -333,28 +394,51 @@ void attn_bwd_16bit(BwdArgs a) {
         f32x4 dvt[NDT], dkt[NDT];
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) dvt[dt] = dkt[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (int qp = 0; qp < nqp; ++qp) {
+        // causal: pairs before kt / 2 end before the tile's first key and add
+        // nothing, unless a query that sees no key (lse = -inf) makes its P
+        // row NaN, which reaches every dV row
+        bool skip_early = a.causal;
+        if (skip_early) {
+            bool e = false;
+            for (int r = lane; r < RQ; r += 64) e |= __builtin_bit_cast(float, lds_ld4(slse + r * 4)) == kNegInf;
+            skip_early = __builtin_amdgcn_ballot_w64(e) == 0;
+        }
+        for (int qp = skip_early ? kt / 2 : 0; qp < nqp; ++qp) {
+            const int q0 = qp * 32;
+            const bool full = kfull && q0 + 31 < a.Sq && (!a.causal || kt * 16 + 15 <= q0);
             float p[8], ds[8];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 const int qt = 2 * qp + hh;
-                // S = Q K^T and dP = dO V^T: rows = queries qt*16 + 4g + i, column = key
-                f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f}, dpacc = f32x4{0.f, 0.f, 0.f, 0.f};
+                // S = Q K^T and dP - delta = dO V^T - delta (accumulated onto
+                // -delta): rows = queries
+                // qt*16 + 4g + i, column = key
+                const f32x4 lse4 = as_f32x4(lds_ld16(slse + (qt * 16 + 4 * g) * 4));
+                const f32x4 ndelta4 = as_f32x4(lds_ld16(sdelta + (qt * 16 + 4 * g) * 4));
+                f32x4 sacc = M::mma(ld_op(sq + qt * 16 * RS, 0), kop[0], f32x4{0.f, 0.f, 0.f, 0.f});
+                f32x4 dpacc = M::mma(ld_op(sdo + qt * 16 * RS, 0), vop[0], ndelta4);
 #pragma unroll
-                for (int i = 0; i < NI; ++i) {
+                for (int i = 1; i < NI; ++i) {
                     sacc = M::mma(ld_op(sq + qt * 16 * RS, i), kop[i], sacc);
                     dpacc = M::mma(ld_op(sdo + qt * 16 * RS, i), vop[i], dpacc);
                 }
-                const f32x4 lse4 = as_f32x4(lds_ld16(slse + (qt * 16 + 4 * g) * 4));
-                const f32x4 delta4 = as_f32x4(lds_ld16(sdelta + (qt * 16 + 4 * g) * 4));
+                if (full) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int q = qt * 16 + 4 * g + i;
-                    const bool ok = kok && q < a.Sq && (!a.causal || key <= q);
-                    const float pv = fast_exp2(sacc[i] * a.c2 - lse4[i]);
-                    // 0 * lse: NaN only for a query that sees no key (lse = -inf)
-                    p[4 * hh + i] = ok ? pv : 0.f * lse4[i];
-                    ds[4 * hh + i] = ok ? pv * (dpacc[i] - delta4[i]) : 0.f;
+                    for (int i = 0; i < 4; ++i) {
+                        const float pv = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse4[i]));
+                        p[4 * hh + i] = pv;
+                        ds[4 * hh + i] = pv * dpacc[i];
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int q = qt * 16 + 4 * g + i;
+                        const bool ok = kok && q < a.Sq && (!a.causal || key <= q);
+                        const float pv = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse4[i]));
+                        // 0 * lse: NaN only for a query that sees no key (lse = -inf)
+                        p[4 * hh + i] = ok ? pv : 0.f * lse4[i];
+                        ds[4 * hh + i] = ok ? pv * dpacc[i] : 0.f;
+                    }
                 }
             }
             const u32x4 pb = {M::pack2(p[0], p[1]), M::pack2(p[2], p[3]), M::pack2(p[4], p[5]), M::pack2(p[6], p[7])};

@@ -78,6 +78,11 @@ struct Mfma16<__bf16> {
     __device__ static inline float to_float(uint16_t bits) {
         return __builtin_bit_cast(float, static_cast<uint32_t>(bits) << 16);
     }
+    // c + a.lo * b.lo + a.hi * b.hi over packed pairs (v_dot2_f32_bf16).
+    __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+    }
 };
 
 template <>
@@ -97,6 +102,11 @@ struct Mfma16<_Float16> {
     }
     __device__ static inline float to_float(uint16_t bits) {
         return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+    }
+    // c + a.lo * b.lo + a.hi * b.hi over packed pairs (v_dot2_f32_f16).
+    __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
     }
 };
 
