@@ -124,6 +124,34 @@ class KqBwdParams(ctypes.Structure):
     ]
 
 
+class MhaParams(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", _i32),
+        ("dtype", _i32),
+        ("batch", _i32),
+        ("seq", _i32),
+        ("embed_dim", _i32),
+        ("num_heads", _i32),
+        ("causal", _i32),
+        ("reserved", _i32),
+        ("x", _ptr),
+        ("x_stride_b", _i64),
+        ("x_stride_s", _i64),
+        ("w_q", _ptr),
+        ("w_k", _ptr),
+        ("w_v", _ptr),
+        ("w_o", _ptr),
+        ("b_q", _ptr),
+        ("b_k", _ptr),
+        ("b_v", _ptr),
+        ("b_o", _ptr),
+        ("y", _ptr),
+        ("y_stride_b", _i64),
+        ("y_stride_s", _i64),
+        ("scale", _f32),
+    ]
+
+
 class DecodeParams(ctypes.Structure):
     _fields_ = [
         ("abi_version", _i32),
@@ -195,6 +223,7 @@ ENTRY_POINTS = {
     "atx_attn_bwd": (ctypes.c_int, [ctypes.POINTER(AttnBwdParams), _ptr]),
     "atx_kq_masked_softmax_fwd": (ctypes.c_int, [ctypes.POINTER(KqParams), _ptr]),
     "atx_kq_bwd": (ctypes.c_int, [ctypes.POINTER(KqBwdParams), _ptr]),
+    "atx_mha_fwd": (ctypes.c_int, [ctypes.POINTER(MhaParams), _ptr]),
     "atx_attn_decode_fwd": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr]),
     "atx_last_error": (ctypes.c_char_p, []),
     "atx_abi_version": (ctypes.c_int, []),

@@ -1,0 +1,436 @@
+// Fused multi-head self-attention layer for gfx950 (bf16 / fp16):
+//   Y = out_proj(attention(q_proj(X), k_proj(X), v_proj(X)))
+// for one sample per workgroup -- the whole of MultiHeadAttention.forward
+// (stratego/networks/attention.py:152-204) with key_value = None, head_dim
+// 64 and num_kv_heads = num_heads.
+//
+// The sample's X rows stay in LDS for the whole layer; Q, K, V of one head at
+// a time are produced into LDS by MFMA, attended over, and the head's output
+// is folded into the output projection, whose fp32 accumulators stay in
+// registers across the heads.  Q, K, V, the attention output and the
+// projection partial sums never leave the CU: HBM sees X once and Y once,
+// and the weights come from L2 (1.2 MB for E = 384, shared by every CU).
+//
+// Per head h (8 waves):
+//  A. [Q_h | K_h | V_h]^T = W_h X^T: 12 feature tiles x NP position tiles,
+//     K = E.  Wave w owns feature tiles 3 (w % 4) .. +2 and half of the
+//     position tiles; the weight operand streams from memory (16-byte loads,
+//     prefetched a few k-steps ahead), X from LDS.  Results are rounded to the
+//     16-bit type (where nn.Linear rounds them) and stored row-major.
+//  B. Attention, one 16-query tile per wave, as the attention kernel does
+//     it: S^T = K Q^T, row softmax in registers, O^T = V^T P^T with V^T from
+//     transposing LDS reads; O (rounded) replaces Q in LDS.
+//  C. Y^T += Wo[:, 64h : 64h + 64] O^T: wave w owns H / 2 feature tiles of
+//     Y for every position.
+// Rounding points match the reference's bf16 modules: Q, K, V and O are
+// rounded to the 16-bit type, every product accumulates in fp32, Y is
+// rounded once at the end.
+#include "ataraxos_attn.h"
+#include "atx_common.hpp"
+
+namespace atx {
+
+struct MhaArgs {
+    const void* x;
+    int64_t xsb;
+    int xss;
+    const void* w[4];  // q, k, v, out: [E, E] row-major (out features x in features)
+    const void* bias[4];
+    void* y;
+    int64_t ysb;
+    int yss;
+    int L;
+    float c2;  // scale * log2(e)
+};
+
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kD = 64;  // head_dim
+#ifndef ATX_MHA_PREFETCH
+#define ATX_MHA_PREFETCH 1
+#endif
+constexpr int PFD = ATX_MHA_PREFETCH;  // k-steps of weight loads in flight ahead of the MFMAs
+
+// Row r of W 16-bit elements (W a multiple of 64): 16-byte chunk c at
+// (c & ~7) | ((c ^ (r >> 1)) & 7).
+template <int W>
+__device__ inline int xoff(int r, int c) {
+    return r * W * 2 + ((c & ~7) | ((c ^ (r >> 1)) & 7)) * 16;
+}
+template <int W>
+__device__ inline int xquad(int r, int e) {
+    return xoff<W>(r, e >> 3) + (e & 7) * 2;
+}
+
+}  // namespace
+
+inline size_t mha_lds_bytes(int E, int np) {
+    const int lp = 16 * np, lv = 32 * ((np + 1) / 2);
+    return (size_t)lp * E * 2 + (size_t)(2 * lp + lv) * kD * 2;
+}
+
+// H heads (even), NP 16-row position tiles (L <= 16 NP).
+template <typename T, int H, int NP, bool CAUSAL>
+__global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
+    using M = Mfma16<T>;
+    constexpr int E = H * kD;
+    constexpr int LP = NP * 16;
+    constexpr int NKC = (NP + 1) / 2;  // 32-key chunks
+    constexpr int LV = NKC * 32;       // V rows staged
+    constexpr int KS = E / 32;         // k-steps of a projection
+    constexpr int PH = (NP + 1) / 2;   // position tiles of a wave in phase A
+    constexpr int FT = H / 2;          // output feature tiles of a wave in phase C
+    constexpr int PF = KS < PFD ? KS : PFD;  // weight prefetch depth (k-steps)
+    constexpr int XC = E / 8;          // 16-byte chunks per X row
+    static_assert(H % 2 == 0 && H <= 8, "H even, at most 8");
+
+    lds_t* const sx = lds_base();
+    lds_t* const sq = sx + LP * E * 2;  // Q_h, then O_h
+    lds_t* const sk = sq + LP * kD * 2;
+    lds_t* const sv = sk + LP * kD * 2;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar descriptors per wave
+    const int m = lane & 15, g = lane >> 4;
+    const int b = blockIdx.x;
+    const int L = a.L;
+    const float kNegInf = -__builtin_inff();
+
+    // ---- X rows (rows past L read 0), V padding rows zeroed --------------------
+    {
+        const rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + b * a.xsb, (uint32_t)(((L - 1) * a.xss + E) * 2));
+        constexpr int N = LP * XC;
+        constexpr int U = (N + kThreads - 1) / kThreads;
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int idx = u * kThreads + tid;
+            const int r = idx / XC, c = idx - (idx / XC) * XC;
+            v[u] = buf_ld16(rx, idx < N ? (uint32_t)(r * a.xss + c * 8) * 2 : 0xfffffff0u);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int idx = u * kThreads + tid;
+            const int r = idx / XC, c = idx - (idx / XC) * XC;
+            if (idx < N) lds_st16(sx + xoff<E>(r, c), v[u]);
+        }
+        for (int idx = tid; idx < (LV - LP) * 8; idx += kThreads)
+            lds_st16(sv + LP * kD * 2 + idx * 16, u32x4{0, 0, 0, 0});
+    }
+
+    // Weight descriptors (each matrix E x E).
+    rsrc_t rw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rw[i] = make_rsrc(a.w[i], (uint32_t)(E * E * 2));
+
+    // Phase C accumulators: Y^T tiles (feature tile wave*FT + f, position tile p).
+    f32x4 yacc[FT][NP];
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) yacc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Phase A roles.
+    const int fg = wave & 3, pg = wave >> 2;
+    const int p0 = pg * PH;
+    // Transposing-read offsets into V (rows 4g + t, elements a4*16 + 4dt).
+    int troff[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) troff[dt] = xquad<kD>(4 * g + (m >> 2), (m & 3) * 16 + 4 * dt);
+
+    __syncthreads();
+
+    for (int h = 0; h < H; ++h) {
+        // ---- A: [Q_h | K_h | V_h]^T for feature tiles 3fg .. 3fg+2 ------------
+        {
+            f32x4 acc[3][PH];
+#pragma unroll
+            for (int f = 0; f < 3; ++f)
+#pragma unroll
+                for (int p = 0; p < PH; ++p) acc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
+            // feature tile ft = 3fg + f: matrix ft / 4, weight row h*64 + (ft % 4)*16 + m
+            uint32_t wrow[3];
+            int wmat[3];
+#pragma unroll
+            for (int f = 0; f < 3; ++f) {
+                const int ft = 3 * fg + f;
+                wmat[f] = ft >> 2;
+                wrow[f] = (uint32_t)((h * kD + (ft & 3) * 16 + m) * E) * 2;
+            }
+            auto wload = [&](int f, int kk) {
+                // rw[] indexed by a runtime matrix: select the descriptor
+                const rsrc_t r = wmat[f] == 0 ? rw[0] : (wmat[f] == 1 ? rw[1] : rw[2]);
+                return buf_ld16(r, wrow[f] + (uint32_t)(kk * 32 + 8 * g) * 2);
+            };
+            u32x4 wbuf[PF][3];
+#pragma unroll
+            for (int s = 0; s < PF; ++s)
+#pragma unroll
+                for (int f = 0; f < 3; ++f) wbuf[s][f] = wload(f, s);
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) {
+                u32x4 xb[PH];
+#pragma unroll
+                for (int p = 0; p < PH; ++p) {
+                    const int pt = p0 + p;
+                    xb[p] = pt < NP ? lds_ld16(sx + xoff<E>(pt * 16 + m, kk * 4 + g)) : u32x4{0, 0, 0, 0};
+                }
+                u32x4 wa[3];
+#pragma unroll
+                for (int f = 0; f < 3; ++f) {
+                    wa[f] = wbuf[kk % PF][f];
+                    if (kk + PF < KS) wbuf[kk % PF][f] = wload(f, kk + PF);
+                }
+#pragma unroll
+                for (int f = 0; f < 3; ++f)
+#pragma unroll
+                    for (int p = 0; p < PH; ++p)
+                        if (p0 + p < NP) acc[f][p] = M::mma(wa[f], xb[p], acc[f][p]);
+            }
+            // bias of the 4 features 4g .. 4g+3 of each tile
+            f32x4 bv[3];
+#pragma unroll
+            for (int f = 0; f < 3; ++f) {
+                bv[f] = f32x4{0.f, 0.f, 0.f, 0.f};
+                const T* bp = static_cast<const T*>(a.bias[wmat[f]]);
+                if (bp) {
+                    const int feat = h * kD + ((3 * fg + f) & 3) * 16 + 4 * g;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) bv[f][i] = static_cast<float>(bp[feat + i]);
+                }
+            }
+            __syncthreads();  // every wave is done reading the previous head's Q / O
+#pragma unroll
+            for (int f = 0; f < 3; ++f) {
+                const int ft = 3 * fg + f;
+                lds_t* const dst = ft < 4 ? sq : (ft < 8 ? sk : sv);
+#pragma unroll
+                for (int p = 0; p < PH; ++p) {
+                    const int pt = p0 + p;
+                    if (pt < NP)
+                        lds_st8(dst + xquad<kD>(pt * 16 + m, (ft & 3) * 16 + 4 * g),
+                                u32x2{M::pack2(acc[f][p][0] + bv[f][0], acc[f][p][1] + bv[f][1]),
+                                      M::pack2(acc[f][p][2] + bv[f][2], acc[f][p][3] + bv[f][3])});
+                }
+            }
+        }
+        __syncthreads();
+
+        // ---- B: attention of head h, one query tile per wave -------------------
+        if (wave < NP) {
+            const int qt = wave;
+            const int qrow = qt * 16 + m;
+            u32x4 qop[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) qop[i] = lds_ld16(sq + xoff<kD>(qrow, 4 * i + g));
+            const int kend = CAUSAL ? min(L, qt * 16 + 16) : L;  // keys >= kend are unusable for the whole tile
+            f32x4 s[NP];
+            float mx = kNegInf;
+#pragma unroll
+            for (int kt = 0; kt < NP; ++kt) {
+                if (kt * 16 < kend) {
+                    f32x4 acc = M::mma(lds_ld16(sk + xoff<kD>(kt * 16 + m, g)), qop[0], f32x4{0.f, 0.f, 0.f, 0.f});
+                    acc = M::mma(lds_ld16(sk + xoff<kD>(kt * 16 + m, 4 + g)), qop[1], acc);
+                    if (kt * 16 + 16 > (CAUSAL ? min(L, qt * 16 + 1) : L)) {
+                        u32x4 ab = __builtin_bit_cast(u32x4, acc);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int key = kt * 16 + 4 * g + i;
+                            const bool ok = key < L && (!CAUSAL || key <= qrow);
+                            ab[i] = ok ? ab[i] : 0xff800000u;
+                        }
+                        acc = __builtin_bit_cast(f32x4, ab);
+                    }
+                    mx = fmaxf(fmaxf(mx, acc[0]), acc[1]);
+                    mx = fmaxf(fmaxf(mx, acc[2]), acc[3]);
+                    s[kt] = acc;
+                }
+            }
+            mx = colgroup_max(mx);
+            const float nb = -mx * a.c2;  // every query sees key 0: mx is finite
+            float sum = 0.f;
+#pragma unroll
+            for (int kt = 0; kt < NP; ++kt) {
+                if (kt * 16 < kend) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        s[kt][i] = fast_exp2(__builtin_fmaf(s[kt][i], a.c2, nb));
+                        sum += s[kt][i];
+                    }
+                }
+            }
+            sum = colgroup_sum(sum);
+            const float rs = 1.f / sum;
+            // P^T packed per 32-key chunk (unnormalised; 1/sum applied to O)
+            u32x4 pk[NKC];
+#pragma unroll
+            for (int c = 0; c < NKC; ++c) {
+                float pv[8];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int kt = 2 * c + hh;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) pv[4 * hh + i] = (kt < NP && kt * 16 < kend) ? s[kt < NP ? kt : 0][i] : 0.f;
+                }
+                pk[c] = u32x4{M::pack2(pv[0], pv[1]), M::pack2(pv[2], pv[3]), M::pack2(pv[4], pv[5]), M::pack2(pv[6], pv[7])};
+            }
+            // O^T = V^T P^T: lane m (query) gets d = 16g + 4dt + i
+            f32x4 o[4];
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int c = 0; c < NKC; ++c) {
+                    if (c * 32 < kend) {
+                        const u32x2 lo = lds_ld8_tr16(sv + 32 * c * kD * 2 + troff[dt]);
+                        const u32x2 hi = lds_ld8_tr16(sv + (32 * c + 16) * kD * 2 + troff[dt]);
+                        acc = M::mma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[c], acc);
+                    }
+                }
+                o[dt] = acc;
+            }
+            // O rows (rounded) replace this tile's Q rows: elements 16g .. 16g+15
+#pragma unroll
+            for (int half = 0; half < 2; ++half)
+                lds_st16(sq + xoff<kD>(qrow, 2 * g + half),
+                         u32x4{M::pack2(o[2 * half][0] * rs, o[2 * half][1] * rs),
+                               M::pack2(o[2 * half][2] * rs, o[2 * half][3] * rs),
+                               M::pack2(o[2 * half + 1][0] * rs, o[2 * half + 1][1] * rs),
+                               M::pack2(o[2 * half + 1][2] * rs, o[2 * half + 1][3] * rs)});
+        }
+        __syncthreads();
+
+        // ---- C: Y^T += Wo[:, 64h .. 64h+63] O_h^T --------------------------------
+        {
+            u32x4 wa[FT][2];
+#pragma unroll
+            for (int f = 0; f < FT; ++f)
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk)
+                    wa[f][kk] = buf_ld16(rw[3], (uint32_t)(((wave * FT + f) * 16 + m) * E + h * kD + kk * 32 + 8 * g) * 2);
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                const u32x4 ob0 = lds_ld16(sq + xoff<kD>(p * 16 + m, g));
+                const u32x4 ob1 = lds_ld16(sq + xoff<kD>(p * 16 + m, 4 + g));
+#pragma unroll
+                for (int f = 0; f < FT; ++f) {
+                    yacc[f][p] = M::mma(wa[f][0], ob0, yacc[f][p]);
+                    yacc[f][p] = M::mma(wa[f][1], ob1, yacc[f][p]);
+                }
+            }
+        }
+    }
+
+    // ---- Y (+ bias), rounded once; rows past L are dropped -------------------------
+    const rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + b * a.ysb, (uint32_t)(((L - 1) * a.yss + E) * 2));
+    const T* const bo = static_cast<const T*>(a.bias[3]);
+#pragma unroll
+    for (int f = 0; f < FT; ++f) {
+        const int feat = (wave * FT + f) * 16 + 4 * g;
+        f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (bo)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bv[i] = static_cast<float>(bo[feat + i]);
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+            buf_st8_cached(ry, (uint32_t)((p * 16 + m) * a.yss + feat) * 2,
+                           u32x2{M::pack2(yacc[f][p][0] + bv[0], yacc[f][p][1] + bv[1]),
+                                 M::pack2(yacc[f][p][2] + bv[2], yacc[f][p][3] + bv[3])});
+    }
+}
+
+namespace {
+
+template <typename K>
+int launch_mha(K kernel, int grid, size_t lds, hipStream_t st, const MhaArgs& a) {
+    if (lds > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) ATX_FAIL(ATX_ERR_LAUNCH, "hipFuncSetAttribute(%zu bytes LDS): %s", lds, hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), lds, st, a);
+    ATX_CHECK_LAUNCH("atx_mha_fwd launch");
+    return ATX_OK;
+}
+
+template <typename T, int H, bool CAUSAL>
+int dispatch_mha_np(int np, int grid, size_t lds, hipStream_t st, const MhaArgs& a) {
+    switch (np) {
+        case 1: return launch_mha(mha_fused<T, H, 1, CAUSAL>, grid, lds, st, a);
+        case 2: return launch_mha(mha_fused<T, H, 2, CAUSAL>, grid, lds, st, a);
+        case 3: return launch_mha(mha_fused<T, H, 3, CAUSAL>, grid, lds, st, a);
+        case 4: return launch_mha(mha_fused<T, H, 4, CAUSAL>, grid, lds, st, a);
+        case 5: return launch_mha(mha_fused<T, H, 5, CAUSAL>, grid, lds, st, a);
+        case 6: return launch_mha(mha_fused<T, H, 6, CAUSAL>, grid, lds, st, a);
+        case 7: return launch_mha(mha_fused<T, H, 7, CAUSAL>, grid, lds, st, a);
+        case 8: return launch_mha(mha_fused<T, H, 8, CAUSAL>, grid, lds, st, a);
+        default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: %d position tiles", np);
+    }
+}
+
+template <typename T, bool CAUSAL>
+int dispatch_mha(int H, int np, int grid, size_t lds, hipStream_t st, const MhaArgs& a) {
+    switch (H) {
+        case 2: return dispatch_mha_np<T, 2, CAUSAL>(np, grid, lds, st, a);
+        case 4: return dispatch_mha_np<T, 4, CAUSAL>(np, grid, lds, st, a);
+        case 6: return dispatch_mha_np<T, 6, CAUSAL>(np, grid, lds, st, a);
+        case 8: return dispatch_mha_np<T, 8, CAUSAL>(np, grid, lds, st, a);
+        default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: %d heads not supported (2, 4, 6, 8)", H);
+    }
+}
+
+}  // namespace
+}  // namespace atx
+
+extern "C" int atx_mha_fwd(const AtxMhaParams* p, void* stream) {
+    using namespace atx;
+    clear_error();
+    if (!p) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: params is NULL");
+    if (p->abi_version != ATX_ABI_VERSION)
+        ATX_FAIL(ATX_ERR_ABI, "atx_mha_fwd: abi_version %d, library is %d", p->abi_version, ATX_ABI_VERSION);
+    if (p->dtype != ATX_DTYPE_BF16 && p->dtype != ATX_DTYPE_FP16) {
+        if (p->dtype == ATX_DTYPE_FP32) ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: fp32 is not supported");
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: unknown dtype %d", p->dtype);
+    }
+    if (p->batch < 1 || p->seq < 1 || p->num_heads < 1)
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: sizes must be >= 1");
+    if (p->embed_dim != p->num_heads * 64)
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: head_dim %d not supported (64)",
+                 p->num_heads > 0 ? p->embed_dim / p->num_heads : 0);
+    if (!p->x || !p->w_q || !p->w_k || !p->w_v || !p->w_o || !p->y)
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: null tensor pointer");
+    if (!(p->scale > 0.f) || p->scale == __builtin_inff())
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: scale must be finite and > 0 (got %g)", (double)p->scale);
+    if (p->seq > 128) ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: seq %d not supported (<= 128)", p->seq);
+    const int E = p->embed_dim, L = p->seq;
+    const int64_t xss = L == 1 ? E : p->x_stride_s, yss = L == 1 ? E : p->y_stride_s;
+    if (!aligned16(p->x) || !aligned16(p->y) || ((p->x_stride_b * 2) & 15) || ((xss * 2) & 15) ||
+        ((p->y_stride_b * 2) & 15) || ((yss * 2) & 15))
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: x/y rows must start on a 16-byte boundary");
+    if (!aligned16(p->w_q) || !aligned16(p->w_k) || !aligned16(p->w_v) || !aligned16(p->w_o))
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: weights must be 16-byte aligned, contiguous [E, E]");
+    if (xss < 0 || yss < E || (int64_t)(L + 16) * xss * 2 + E * 2 > 0x7fffffffLL ||
+        (int64_t)(L + 16) * yss * 2 + E * 2 > 0x7fffffffLL)
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: row strides must be >= 0 (y: >= embed_dim) and one sample < 2 GiB");
+    const int np = (L + 15) / 16;
+    const size_t lds = mha_lds_bytes(E, np);
+    if (lds > 160 * 1024)
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: seq %d, embed_dim %d need %zu bytes of LDS (> 160 KiB)", L, E, lds);
+
+    MhaArgs a;
+    a.x = p->x; a.xsb = p->x_stride_b; a.xss = (int)xss;
+    a.w[0] = p->w_q; a.w[1] = p->w_k; a.w[2] = p->w_v; a.w[3] = p->w_o;
+    a.bias[0] = p->b_q; a.bias[1] = p->b_k; a.bias[2] = p->b_v; a.bias[3] = p->b_o;
+    a.y = p->y; a.ysb = p->y_stride_b; a.yss = (int)yss;
+    a.L = L;
+    a.c2 = p->scale * kLog2e;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int H = p->num_heads;
+    if (p->dtype == ATX_DTYPE_BF16)
+        return p->causal ? dispatch_mha<__bf16, true>(H, np, p->batch, lds, st, a)
+                         : dispatch_mha<__bf16, false>(H, np, p->batch, lds, st, a);
+    return p->causal ? dispatch_mha<_Float16, true>(H, np, p->batch, lds, st, a)
+                     : dispatch_mha<_Float16, false>(H, np, p->batch, lds, st, a);
+}

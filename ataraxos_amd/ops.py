@@ -15,6 +15,8 @@ outside the kernels' range raises.
   ``stratego/training/selfplay.py:284``).
 * :func:`kq_policy_backward` — its dq, dk for the gradient of the logits or
   of the probabilities, in one launch.
+* :func:`mha_forward` — a whole self-attention layer (projections, attention,
+  output projection) in one launch, ``stratego/networks/attention.py:152-204``.
 * :func:`attention_decode` — one query per (batch, head) against a KV cache.
 """
 
@@ -398,6 +400,88 @@ def kq_policy_backward(
     p.scale = float(scale)
     _lib.check(_lib.call("atx_kq_bwd", p, _stream(q)), "atx_kq_bwd")
     return dq, dk
+
+
+MHA_HEADS = (2, 4, 6, 8)
+
+
+def _mha_lds_bytes(embed_dim: int, seq: int) -> int:
+    np_ = -(-seq // 16)
+    return np_ * 16 * embed_dim * 2 + (2 * np_ * 16 + 32 * ((np_ + 1) // 2)) * 64 * 2
+
+
+def mha_forward_supported(embed_dim: int, num_heads: int, seq: int, dtype: torch.dtype) -> bool:
+    """True when :func:`mha_forward` covers this layer: bf16/fp16, head_dim
+    64, 2/4/6/8 heads, up to 128 positions within 160 KiB of LDS."""
+    return (
+        dtype in _BWD_DTYPES
+        and num_heads in MHA_HEADS
+        and embed_dim == 64 * num_heads
+        and 1 <= seq <= 128
+        and _mha_lds_bytes(embed_dim, seq) <= _LDS_BYTES
+    )
+
+
+def mha_forward(
+    x: torch.Tensor,
+    w_q: torch.Tensor,
+    w_k: torch.Tensor,
+    w_v: torch.Tensor,
+    w_o: torch.Tensor,
+    num_heads: int,
+    b_q: torch.Tensor | None = None,
+    b_k: torch.Tensor | None = None,
+    b_v: torch.Tensor | None = None,
+    b_o: torch.Tensor | None = None,
+    causal: bool = False,
+    scale: float | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Whole self-attention layer in one launch (no autograd):
+    ``out_proj(attention(q_proj(x), k_proj(x), v_proj(x)))`` with the
+    ``nn.Linear`` weights ``[E, E]`` and optional biases ``[E]``.  x ``[B, L, E]``
+    -> ``[B, L, E]`` in x's dtype.  Q, K, V and the attention output are
+    rounded to x's dtype, as the reference's bf16 modules round them."""
+    _require_device("mha_forward", x, w_q, w_k, w_v, w_o)
+    if x.dim() != 3:
+        raise ValueError("mha_forward: x must be [batch, seq, embed_dim]")
+    b, l, e = x.shape
+    for name, w in (("w_q", w_q), ("w_k", w_k), ("w_v", w_v), ("w_o", w_o)):
+        if tuple(w.shape) != (e, e) or w.dtype != x.dtype:
+            raise ValueError(f"mha_forward: {name} must be [{e}, {e}] in {x.dtype}")
+    if not mha_forward_supported(e, num_heads, l, x.dtype):
+        raise NotImplementedError(
+            f"mha_forward: {x.dtype}, embed_dim {e}, {num_heads} heads, seq {l} not covered by the fused kernel"
+        )
+    biases = []
+    for name, t in (("b_q", b_q), ("b_k", b_k), ("b_v", b_v), ("b_o", b_o)):
+        if t is not None:
+            if tuple(t.shape) != (e,) or t.dtype != x.dtype:
+                raise ValueError(f"mha_forward: {name} must be [{e}] in {x.dtype}")
+            _require_device("mha_forward", x, t)
+            t = t.contiguous()
+        biases.append(t)
+    x = _aligned_rows(x)
+    ws = [w.contiguous() if not w.is_contiguous() or w.data_ptr() % 16 else w for w in (w_q, w_k, w_v, w_o)]
+    if out is None:
+        out = torch.empty((b, l, e), dtype=x.dtype, device=x.device)
+    elif tuple(out.shape) != (b, l, e) or out.dtype != x.dtype or out.stride(-1) != 1:
+        raise ValueError("mha_forward: out has the wrong shape, dtype or layout")
+    if scale is None:
+        scale = 1.0 / 8.0  # 1 / sqrt(head_dim = 64)
+
+    p = _lib.MhaParams()
+    p.abi_version = _lib.ABI_VERSION
+    p.dtype = _DTYPES[x.dtype]
+    p.batch, p.seq, p.embed_dim, p.num_heads = b, l, e, num_heads
+    p.causal = 1 if causal else 0
+    p.x, p.x_stride_b, p.x_stride_s = x.data_ptr(), x.stride(0), x.stride(1)
+    p.w_q, p.w_k, p.w_v, p.w_o = (w.data_ptr() for w in ws)
+    p.b_q, p.b_k, p.b_v, p.b_o = (t.data_ptr() if t is not None else None for t in biases)
+    p.y, p.y_stride_b, p.y_stride_s = out.data_ptr(), out.stride(0), out.stride(1)
+    p.scale = float(scale)
+    _lib.check(_lib.call("atx_mha_fwd", p, _stream(x)), "atx_mha_fwd")
+    return out
 
 
 def attention_decode(

@@ -241,6 +241,53 @@ typedef struct AtxKqBwdParams {
 int atx_kq_bwd(const AtxKqBwdParams* params, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Fused self-attention layer: projections + attention + output projection  */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * For every sample b (x, y: [batch, seq, embed_dim], rows contiguous):
+ *   q = x Wq^T + bq, k = x Wk^T + bk, v = x Wv^T + bv   (rounded to dtype)
+ *   o = per head softmax(scale * q_h k_h^T [+ top-left causal mask]) v_h
+ *                                                        (rounded to dtype)
+ *   y = o Wo^T + bo
+ * with W* the nn.Linear weights [embed_dim, embed_dim] (out x in,
+ * contiguous) and b* optional biases [embed_dim] (NULL = none).
+ * head_dim 64 (embed_dim = 64 * num_heads), num_heads in {2, 4, 6, 8},
+ * seq <= 128 within 160 KiB of LDS (embed_dim 512: seq <= 112), 16-bit only.
+ */
+typedef struct AtxMhaParams {
+    int32_t abi_version;
+    int32_t dtype; /* ATX_DTYPE_BF16 or FP16: x, weights, biases and y */
+    int32_t batch;
+    int32_t seq;
+    int32_t embed_dim;
+    int32_t num_heads;
+    int32_t causal;
+    int32_t reserved; /* 0 */
+    const void* x;
+    int64_t x_stride_b, x_stride_s;
+    const void* w_q;
+    const void* w_k;
+    const void* w_v;
+    const void* w_o;
+    const void* b_q; /* optional */
+    const void* b_k;
+    const void* b_v;
+    const void* b_o;
+    void* y;
+    int64_t y_stride_b, y_stride_s;
+    float scale; /* the reference uses 1 / sqrt(head_dim) */
+} AtxMhaParams;
+
+/*
+ * Replaces MultiHeadAttention.forward for self-attention
+ * (stratego/networks/attention.py:152-204 with key_value = None): the
+ * q/k/v projections (:175-179), the backend dispatch (:192-200) and the
+ * output projection (:203-204), in one launch.
+ */
+int atx_mha_fwd(const AtxMhaParams* params, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Single-query attention over a KV cache (incremental decode)              */
 /* ------------------------------------------------------------------------ */
 

@@ -28,6 +28,7 @@ STRUCTS = {
     "AtxAttnBwdParams": _lib.AttnBwdParams,
     "AtxKqParams": _lib.KqParams,
     "AtxKqBwdParams": _lib.KqBwdParams,
+    "AtxMhaParams": _lib.MhaParams,
     "AtxDecodeParams": _lib.DecodeParams,
 }
 
@@ -237,6 +238,34 @@ def test_policy_backward_validation_codes():
         setattr(p, field, value)
         _expect("atx_kq_bwd", p, code, text)
         setattr(p, field, saved)
+
+
+def test_fused_layer_validation_codes():
+    p = _lib.MhaParams()
+    p.abi_version, p.dtype, p.batch, p.seq, p.embed_dim, p.num_heads = _lib.ABI_VERSION, _lib.DTYPE_BF16, 4, 100, 384, 6
+    p.x = p.w_q = p.w_k = p.w_v = p.w_o = p.y = 1 << 20  # never dereferenced: every case fails validation
+    p.x_stride_b = p.y_stride_b = 100 * 384
+    p.x_stride_s = p.y_stride_s = 384
+    p.scale = 0.125
+    assert _lib.load().atx_mha_fwd(None, None) == _lib.ERR_INVALID_ARGUMENT
+    for field, value, code, text in [
+        ("abi_version", 3, _lib.ERR_ABI, "abi_version"),
+        ("dtype", _lib.DTYPE_FP32, _lib.ERR_UNSUPPORTED, "fp32"),
+        ("embed_dim", 400, _lib.ERR_UNSUPPORTED, "head_dim"),
+        ("num_heads", 3, _lib.ERR_UNSUPPORTED, "head_dim"),
+        ("seq", 129, _lib.ERR_UNSUPPORTED, "seq"),
+        ("w_o", None, _lib.ERR_INVALID_ARGUMENT, "null"),
+        ("scale", -1.0, _lib.ERR_INVALID_ARGUMENT, "scale"),
+        ("x_stride_s", 388, _lib.ERR_INVALID_ARGUMENT, "16-byte"),
+        ("y_stride_s", 192, _lib.ERR_INVALID_ARGUMENT, "strides"),
+    ]:
+        saved = getattr(p, field)
+        setattr(p, field, value)
+        _expect("atx_mha_fwd", p, code, text)
+        setattr(p, field, saved)
+    p.embed_dim, p.num_heads, p.seq = 512, 8, 128
+    p.x_stride_s = p.y_stride_s = 512
+    _expect("atx_mha_fwd", p, _lib.ERR_UNSUPPORTED, "LDS")
 
 
 def test_decode_validation_codes():

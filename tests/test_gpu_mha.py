@@ -1,0 +1,143 @@
+"""Parity of the fused self-attention layer (``atx_mha_fwd``) against the
+float64 oracle's module forward (``oracle.attention.mha_forward``, which
+restates stratego/networks/attention.py:152-204).
+
+Inputs and weights are drawn on the CPU from seeded generators and rounded to
+the kernel's 16-bit dtype; the oracle runs in float64 on the same values.
+Tolerance: the contract's 16-bit figure, ``max|y - ref| <= 2e-2``, plus a
+normwise ``max|y - ref| <= 2e-2 * max|ref|``, since the layer rounds Q, K, V and
+the attention output to 16 bits where the reference's bf16 modules do.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from ataraxos_amd import MultiHeadAttention, ops
+from oracle.attention import mha_forward as oracle_mha
+from tests._cases import randn, to_np64
+
+pytestmark = pytest.mark.gpu
+
+
+def _announce(msg: str) -> None:
+    print(f"\n[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def layer(e, dtype, seed, bias=False):
+    g = torch.Generator().manual_seed(seed)
+    bound = e**-0.5  # nn.Linear's default init range
+    ws = [((torch.rand(e, e, generator=g) * 2 - 1) * bound).to(dtype) for _ in range(4)]
+    bs = [((torch.rand(e, generator=g) * 2 - 1) * bound).to(dtype) for _ in range(4)] if bias else [None] * 4
+    return ws, bs
+
+
+def run_case(cuda, b, l, h, dtype=torch.bfloat16, causal=False, bias=False, seed=0, x_view=False):
+    e = 64 * h
+    _announce(f"mha b={b} l={l} h={h} {dtype} causal={causal} bias={bias} view={x_view}")
+    x = randn((b, l, e), seed, dtype)
+    ws, bs = layer(e, dtype, seed + 1, bias)
+    if x_view:  # rows of a wider buffer, NaN after the sequence and in the padding columns
+        big = torch.full((b, l + 5, e + 64), float("nan"), dtype=dtype)
+        big[:, :l, :e] = x
+        xd = big.to(cuda)[:, :l, :e]
+    else:
+        xd = x.to(cuda)
+    wd = [w.to(cuda) for w in ws]
+    bd = [t.to(cuda) if t is not None else None for t in bs]
+    y = ops.mha_forward(xd, *wd, num_heads=h, b_q=bd[0], b_k=bd[1], b_v=bd[2], b_o=bd[3], causal=causal)
+    torch.cuda.synchronize()
+    names = ("q_proj", "k_proj", "v_proj", "out_proj")
+    weights = {f"{n}.weight": to_np64(w) for n, w in zip(names, ws)}
+    if bias:
+        weights.update({f"{n}.bias": to_np64(t) for n, t in zip(names, bs)})
+    ref = oracle_mha(to_np64(x), None, weights, h, causal=causal)
+    got = to_np64(y)
+    assert np.isfinite(got).all(), "non-finite output"
+    err = float(np.max(np.abs(got - ref)))
+    assert err <= 2e-2, f"max-abs {err:.3e}"
+    assert err <= 2e-2 * float(np.max(np.abs(ref))), f"normwise {err:.3e} vs {np.max(np.abs(ref)):.3e}"
+    return err
+
+
+def test_move_net_layer(cuda):
+    """C3 layer shape: L=100, E=384, 6 x 64, bf16."""
+    run_case(cuda, 32, 100, 6, seed=1)
+
+
+@pytest.mark.parametrize("h", [2, 4, 6, 8])
+def test_heads(cuda, h):
+    run_case(cuda, 4, 100, h, seed=10 + h)
+
+
+@pytest.mark.parametrize("l", [1, 2, 15, 16, 17, 33, 40, 64, 97, 112, 128])
+def test_seq_lengths(cuda, l):
+    run_case(cuda, 3, l, 4, seed=20 + l)
+
+
+@pytest.mark.parametrize("l", [1, 17, 40, 100])
+def test_causal(cuda, l):
+    """Setup network: causal self-attention (40 pieces)."""
+    run_case(cuda, 4, l, 6, causal=True, seed=40 + l)
+
+
+def test_biases_and_fp16(cuda):
+    run_case(cuda, 4, 100, 6, bias=True, seed=50)
+    run_case(cuda, 4, 100, 6, dtype=torch.float16, seed=51)
+    run_case(cuda, 4, 40, 8, dtype=torch.float16, bias=True, causal=True, seed=52)
+
+
+def test_strided_input_and_guard_values(cuda):
+    """x as a view into a wider buffer holding NaN past the sequence and in the
+    columns beyond E: nothing outside the view is read."""
+    run_case(cuda, 4, 100, 6, x_view=True, seed=60)
+
+
+def test_rows_past_the_sequence_are_not_written(cuda):
+    _announce("mha output guard rows")
+    b, l, h = 3, 40, 6
+    e = 64 * h
+    x = randn((b, l, e), 61, torch.bfloat16).to(cuda)
+    ws, _ = layer(e, torch.bfloat16, 62)
+    out_big = torch.full((b, l + 8, e), 7.0, dtype=torch.bfloat16, device=cuda)
+    ops.mha_forward(x, *[w.to(cuda) for w in ws], num_heads=h, out=out_big[:, :l])
+    torch.cuda.synchronize()
+    assert (out_big[:, l:] == 7.0).all()
+
+
+def test_matches_the_unfused_module_path(cuda):
+    """The fused layer equals MultiHeadAttention's unfused GPU path
+    (hipBLASLt projections + the attention kernel) to bf16 rounding."""
+    _announce("mha vs unfused module")
+    torch.manual_seed(7)
+    m = MultiHeadAttention(384, 6).to(cuda, torch.bfloat16).eval()
+    x = randn((16, 100, 384), 70, torch.bfloat16).to(cuda)
+    with torch.no_grad():
+        unfused = m(x)
+        fused = ops.mha_forward(x, m.q_proj.weight, m.k_proj.weight, m.v_proj.weight, m.out_proj.weight, num_heads=6)
+    err = (fused.float() - unfused.float()).abs().max().item()
+    assert err <= 2e-2 * unfused.float().abs().max().item(), err
+
+
+def test_deterministic(cuda):
+    x = randn((64, 100, 384), 80, torch.bfloat16).to(cuda)
+    ws = [w.to(cuda) for w in layer(384, torch.bfloat16, 81)[0]]
+    a = ops.mha_forward(x, *ws, num_heads=6)
+    b = ops.mha_forward(x, *ws, num_heads=6)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_rejects_unsupported(cuda):
+    x = torch.zeros(2, 10, 384, device=cuda)
+    w = torch.zeros(384, 384, device=cuda)
+    with pytest.raises(NotImplementedError):
+        ops.mha_forward(x, w, w, w, w, num_heads=6)  # fp32
+    xb, wb = x.bfloat16(), w.bfloat16()
+    with pytest.raises(NotImplementedError):
+        ops.mha_forward(xb, wb, wb, wb, wb, num_heads=3)  # head_dim 128
