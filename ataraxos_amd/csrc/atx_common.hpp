@@ -148,10 +148,13 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ inline rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
-constexpr int kAuxNt = 2;  // cache-policy bit of the streaming (nontemporal) hint
+constexpr int kAuxNt = 2;   // cache-policy bit of the streaming (nontemporal) hint
+constexpr int kAuxGlc = 1;  // globally coherent: the load bypasses the CU's L1
 __device__ inline u32x4 buf_ld16(rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, ATX_STREAM_LOADS ? kAuxNt : 0);
 }
+// Load without the streaming hint, for data many workgroups re-read (weights).
+__device__ inline u32x4 buf_ld16_keep(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0); }
 __device__ inline void buf_st16(rsrc_t r, uint32_t off, u32x4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, ATX_STREAM_STORES ? kAuxNt : 0);
 }

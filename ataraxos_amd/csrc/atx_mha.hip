@@ -4,12 +4,14 @@
 // (stratego/networks/attention.py:152-204) with key_value = None, head_dim
 // 64 and num_kv_heads = num_heads.
 //
-// The sample's X rows stay in LDS for the whole layer; Q, K, V of one head at
-// a time are produced into LDS by MFMA, attended over, and the head's output
-// is folded into the output projection, whose fp32 accumulators stay in
-// registers across the heads.  Q, K, V, the attention output and the
-// projection partial sums never leave the CU: HBM sees X once and Y once,
-// and the weights come from L2 (1.2 MB for E = 384, shared by every CU).
+// The sample's X rows stay in LDS while Q, K, V of one head at a time are
+// produced into LDS by MFMA and attended over; each head's output (the
+// reference's attn_out columns 64h .. 64h+63) is parked in the sample's rows
+// of y, which the workgroup alone owns.  After the last head those rows come
+// back into LDS in place of X and the output projection runs as one GEMM over
+// all heads.  Q, K, V never leave the CU; HBM sees X once and Y once (the
+// parked attention output stays in the caches), and the weights come from L2
+// (1.2 MB for E = 384, shared by every CU).
 //
 // Per head h (8 waves):
 //  A. [Q_h | K_h | V_h]^T = W_h X^T: 12 feature tiles x NP position tiles,
@@ -19,9 +21,9 @@
 //     16-bit type (where nn.Linear rounds them) and stored row-major.
 //  B. Attention, one 16-query tile per wave, as the attention kernel does
 //     it: S^T = K Q^T, row softmax in registers, O^T = V^T P^T with V^T from
-//     transposing LDS reads; O (rounded) replaces Q in LDS.
-//  C. Y^T += Wo[:, 64h : 64h + 64] O^T: wave w owns H / 2 feature tiles of
-//     Y for every position.
+//     transposing LDS reads; O is rounded and stored to y.
+// Then Y^T = Wo O^T with wave w owning H / 2 feature tiles of Y for every
+// position, and Y (+ bias) overwrites the parked O.
 // Rounding points match the reference's bf16 modules: Q, K, V and O are
 // rounded to the 16-bit type, every product accumulates in fp32, Y is
 // rounded once at the end.
@@ -48,12 +50,11 @@ namespace {
 constexpr int kThreads = 512;
 constexpr int kD = 64;  // head_dim
 #ifndef ATX_MHA_PREFETCH
-#define ATX_MHA_PREFETCH 1
+#define ATX_MHA_PREFETCH 2
 #endif
 constexpr int PFD = ATX_MHA_PREFETCH;  // k-steps of weight loads in flight ahead of the MFMAs
 
-// Row r of W 16-bit elements (W a multiple of 64): 16-byte chunk c at
-// (c & ~7) | ((c ^ (r >> 1)) & 7).
+// Row r of 64 16-bit elements (Q, K, V): 16-byte chunk c at c ^ ((r >> 1) & 7).
 template <int W>
 __device__ inline int xoff(int r, int c) {
     return r * W * 2 + ((c & ~7) | ((c ^ (r >> 1)) & 7)) * 16;
@@ -61,6 +62,13 @@ __device__ inline int xoff(int r, int c) {
 template <int W>
 __device__ inline int xquad(int r, int e) {
     return xoff<W>(r, e >> 3) + (e & 7) * 2;
+}
+// Row r of E 16-bit elements (X, then O; E a multiple of 128): chunk c at
+// (c & ~15) | ((c ^ r) & 15).  An operand read (rows 16p + m, one chunk per
+// 16-lane group) then covers all 16 bank groups of a 256-byte LDS cycle.
+template <int W>
+__device__ inline int eoff(int r, int c) {
+    return r * W * 2 + ((c & ~15) | ((c ^ r) & 15)) * 16;
 }
 
 }  // namespace
@@ -114,31 +122,38 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
         for (int u = 0; u < U; ++u) {
             const int idx = u * kThreads + tid;
             const int r = idx / XC, c = idx - (idx / XC) * XC;
-            if (idx < N) lds_st16(sx + xoff<E>(r, c), v[u]);
+            if (idx < N) lds_st16(sx + eoff<E>(r, c), v[u]);
         }
         for (int idx = tid; idx < (LV - LP) * 8; idx += kThreads)
             lds_st16(sv + LP * kD * 2 + idx * 16, u32x4{0, 0, 0, 0});
     }
 
+    const rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + b * a.ysb, (uint32_t)(((L - 1) * a.yss + E) * 2));
     // Weight descriptors (each matrix E x E).
     rsrc_t rw[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) rw[i] = make_rsrc(a.w[i], (uint32_t)(E * E * 2));
 
-    // Phase C accumulators: Y^T tiles (feature tile wave*FT + f, position tile p).
-    f32x4 yacc[FT][NP];
-#pragma unroll
-    for (int f = 0; f < FT; ++f)
-#pragma unroll
-        for (int p = 0; p < NP; ++p) yacc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
-
     // Phase A roles.
     const int fg = wave & 3, pg = wave >> 2;
+    // Phase A position tiles p0 .. p0 + PH - 1; with NP odd the second group's
+    // last tile repeats tile NP - 1 (computed, never stored) so that the
+    // MFMA loop has no per-tile tests.
     const int p0 = pg * PH;
+    int xpos[PH];
+#pragma unroll
+    for (int p = 0; p < PH; ++p) xpos[p] = min(p0 + p, NP - 1) * 16 * E * 2;
     // Transposing-read offsets into V (rows 4g + t, elements a4*16 + 4dt).
     int troff[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) troff[dt] = xquad<kD>(4 * g + (m >> 2), (m & 3) * 16 + 4 * dt);
+
+    // X / O rows in LDS: row pt*16 + m, logical chunk kk*4 + g sits at
+    // xlane[kk & 3] + pt*16*E*2 + (kk >> 2)*256 (the swizzle term depends on
+    // m only, since 16 pt is a multiple of 16).
+    int xlane[4];
+#pragma unroll
+    for (int par = 0; par < 4; ++par) xlane[par] = m * E * 2 + (((4 * par + g) ^ m) & 15) * 16;
 
     __syncthreads();
 
@@ -151,69 +166,66 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
 #pragma unroll
                 for (int p = 0; p < PH; ++p) acc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
             // feature tile ft = 3fg + f: matrix ft / 4, weight row h*64 + (ft % 4)*16 + m
+            rsrc_t wr[3];
             uint32_t wrow[3];
-            int wmat[3];
 #pragma unroll
             for (int f = 0; f < 3; ++f) {
                 const int ft = 3 * fg + f;
-                wmat[f] = ft >> 2;
-                wrow[f] = (uint32_t)((h * kD + (ft & 3) * 16 + m) * E) * 2;
+                wr[f] = (ft >> 2) == 0 ? rw[0] : ((ft >> 2) == 1 ? rw[1] : rw[2]);
+                wrow[f] = (uint32_t)((h * kD + (ft & 3) * 16 + m) * E + 8 * g) * 2;
             }
-            auto wload = [&](int f, int kk) {
-                // rw[] indexed by a runtime matrix: select the descriptor
-                const rsrc_t r = wmat[f] == 0 ? rw[0] : (wmat[f] == 1 ? rw[1] : rw[2]);
-                return buf_ld16(r, wrow[f] + (uint32_t)(kk * 32 + 8 * g) * 2);
-            };
+            // Weight k-steps stay PF ahead of the MFMAs: each iteration issues
+            // step kk + PF first, and a scheduling barrier keeps the compiler
+            // from sinking those loads next to their use.
             u32x4 wbuf[PF][3];
 #pragma unroll
-            for (int s = 0; s < PF; ++s)
+            for (int s2 = 0; s2 < PF; ++s2)
 #pragma unroll
-                for (int f = 0; f < 3; ++f) wbuf[s][f] = wload(f, s);
+                for (int f = 0; f < 3; ++f) wbuf[s2][f] = buf_ld16_keep(wr[f], wrow[f] + s2 * 64);
 #pragma unroll
             for (int kk = 0; kk < KS; ++kk) {
-                u32x4 xb[PH];
-#pragma unroll
-                for (int p = 0; p < PH; ++p) {
-                    const int pt = p0 + p;
-                    xb[p] = pt < NP ? lds_ld16(sx + xoff<E>(pt * 16 + m, kk * 4 + g)) : u32x4{0, 0, 0, 0};
-                }
-                u32x4 wa[3];
+                u32x4 wa[3], nxt[3];
 #pragma unroll
                 for (int f = 0; f < 3; ++f) {
                     wa[f] = wbuf[kk % PF][f];
-                    if (kk + PF < KS) wbuf[kk % PF][f] = wload(f, kk + PF);
+                    if (kk + PF < KS) nxt[f] = buf_ld16_keep(wr[f], wrow[f] + (kk + PF) * 64);
                 }
+                __builtin_amdgcn_sched_barrier(0);
+                u32x4 xb[PH];
+#pragma unroll
+                for (int p = 0; p < PH; ++p) xb[p] = lds_ld16(sx + xlane[kk & 3] + xpos[p] + (kk >> 2) * 256);
 #pragma unroll
                 for (int f = 0; f < 3; ++f)
 #pragma unroll
-                    for (int p = 0; p < PH; ++p)
-                        if (p0 + p < NP) acc[f][p] = M::mma(wa[f], xb[p], acc[f][p]);
+                    for (int p = 0; p < PH; ++p) acc[f][p] = M::mma(wa[f], xb[p], acc[f][p]);
+                if (kk + PF < KS)
+#pragma unroll
+                    for (int f = 0; f < 3; ++f) wbuf[kk % PF][f] = nxt[f];
             }
             // bias of the 4 features 4g .. 4g+3 of each tile
             f32x4 bv[3];
 #pragma unroll
             for (int f = 0; f < 3; ++f) {
                 bv[f] = f32x4{0.f, 0.f, 0.f, 0.f};
-                const T* bp = static_cast<const T*>(a.bias[wmat[f]]);
+                const int ft = 3 * fg + f;
+                const T* bp = static_cast<const T*>(a.bias[ft >> 2]);
                 if (bp) {
-                    const int feat = h * kD + ((3 * fg + f) & 3) * 16 + 4 * g;
+                    const int feat = h * kD + (ft & 3) * 16 + 4 * g;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) bv[f][i] = static_cast<float>(bp[feat + i]);
                 }
             }
-            __syncthreads();  // every wave is done reading the previous head's Q / O
+            __syncthreads();  // every wave is done with the previous head's Q, K, V
 #pragma unroll
             for (int f = 0; f < 3; ++f) {
                 const int ft = 3 * fg + f;
                 lds_t* const dst = ft < 4 ? sq : (ft < 8 ? sk : sv);
 #pragma unroll
-                for (int p = 0; p < PH; ++p) {
-                    const int pt = p0 + p;
-                    if (pt < NP)
-                        lds_st8(dst + xquad<kD>(pt * 16 + m, (ft & 3) * 16 + 4 * g),
+                for (int p = 0; p < PH; ++p)
+                    if (p0 + p < NP)
+                        lds_st8(dst + xquad<kD>((p0 + p) * 16 + m, (ft & 3) * 16 + 4 * g),
                                 u32x2{M::pack2(acc[f][p][0] + bv[f][0], acc[f][p][1] + bv[f][1]),
                                       M::pack2(acc[f][p][2] + bv[f][2], acc[f][p][3] + bv[f][3])});
-                }
             }
         }
         __syncthreads();
@@ -291,40 +303,85 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
                 }
                 o[dt] = acc;
             }
-            // O rows (rounded) replace this tile's Q rows: elements 16g .. 16g+15
+            // O rows (rounded) go to y, which holds the sample's attention output
+            // [L, E] until the output projection overwrites it: elements
+            // 64h + 16g .. +15 of row qrow (rows past L are dropped)
 #pragma unroll
             for (int half = 0; half < 2; ++half)
-                lds_st16(sq + xoff<kD>(qrow, 2 * g + half),
-                         u32x4{M::pack2(o[2 * half][0] * rs, o[2 * half][1] * rs),
-                               M::pack2(o[2 * half][2] * rs, o[2 * half][3] * rs),
-                               M::pack2(o[2 * half + 1][0] * rs, o[2 * half + 1][1] * rs),
-                               M::pack2(o[2 * half + 1][2] * rs, o[2 * half + 1][3] * rs)});
+                buf_st16_cached(ry, (uint32_t)(qrow * a.yss + h * kD + 16 * g + 8 * half) * 2,
+                                u32x4{M::pack2(o[2 * half][0] * rs, o[2 * half][1] * rs),
+                                      M::pack2(o[2 * half][2] * rs, o[2 * half][3] * rs),
+                                      M::pack2(o[2 * half + 1][0] * rs, o[2 * half + 1][1] * rs),
+                                      M::pack2(o[2 * half + 1][2] * rs, o[2 * half + 1][3] * rs)});
         }
-        __syncthreads();
+    }
+    // Every head's O store has completed (s_waitcnt 0: acknowledged by the
+    // L2 this CU writes through) before any wave of the workgroup reads the
+    // rows back with L1-bypassing loads.  Only this workgroup touches these
+    // rows, so no wider fence (which would write back and invalidate L2) is
+    // needed.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
 
-        // ---- C: Y^T += Wo[:, 64h .. 64h+63] O_h^T --------------------------------
-        {
-            u32x4 wa[FT][2];
+    // ---- O (all heads) back into LDS in place of X: reads bypass L1 ------------------
+    {
+        constexpr int N = LP * XC;
+        constexpr int U = (N + kThreads - 1) / kThreads;
+        u32x4 v[U];
 #pragma unroll
-            for (int f = 0; f < FT; ++f)
+        for (int u = 0; u < U; ++u) {
+            const int idx = u * kThreads + tid;
+            const int r = idx / XC, c = idx - (idx / XC) * XC;
+            v[u] = __builtin_amdgcn_raw_buffer_load_b128(ry, (int)(idx < N ? (uint32_t)(r * a.yss + c * 8) * 2 : 0xfffffff0u),
+                                                         0, kAuxGlc);
+        }
 #pragma unroll
-                for (int kk = 0; kk < 2; ++kk)
-                    wa[f][kk] = buf_ld16(rw[3], (uint32_t)(((wave * FT + f) * 16 + m) * E + h * kD + kk * 32 + 8 * g) * 2);
+        for (int u = 0; u < U; ++u) {
+            const int idx = u * kThreads + tid;
+            const int r = idx / XC, c = idx - (idx / XC) * XC;
+            if (idx < N) lds_st16(sx + eoff<E>(r, c), v[u]);
+        }
+    }
+    __syncthreads();
+
+    // ---- Y^T = Wo O^T: wave w owns feature tiles FT w .. FT w + FT-1 -----------------
+    f32x4 yacc[FT][NP];
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) yacc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
+    {
+        uint32_t orow[FT];
+#pragma unroll
+        for (int f = 0; f < FT; ++f) orow[f] = (uint32_t)(((wave * FT + f) * 16 + m) * E) * 2;
+        constexpr int PFO = KS < PFD ? KS : PFD;
+        u32x4 wbuf[PFO][FT];
+#pragma unroll
+        for (int s2 = 0; s2 < PFO; ++s2)
+#pragma unroll
+            for (int f = 0; f < FT; ++f) wbuf[s2][f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)(s2 * 32 + 8 * g) * 2);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            u32x4 wa[FT], nxt[FT];
+#pragma unroll
+            for (int f = 0; f < FT; ++f) {
+                wa[f] = wbuf[kk % PFO][f];
+                if (kk + PFO < KS) nxt[f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)((kk + PFO) * 32 + 8 * g) * 2);
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
-                const u32x4 ob0 = lds_ld16(sq + xoff<kD>(p * 16 + m, g));
-                const u32x4 ob1 = lds_ld16(sq + xoff<kD>(p * 16 + m, 4 + g));
+                const u32x4 ob = lds_ld16(sx + xlane[kk & 3] + p * 16 * E * 2 + (kk >> 2) * 256);
 #pragma unroll
-                for (int f = 0; f < FT; ++f) {
-                    yacc[f][p] = M::mma(wa[f][0], ob0, yacc[f][p]);
-                    yacc[f][p] = M::mma(wa[f][1], ob1, yacc[f][p]);
-                }
+                for (int f = 0; f < FT; ++f) yacc[f][p] = M::mma(wa[f], ob, yacc[f][p]);
             }
+            if (kk + PFO < KS)
+#pragma unroll
+                for (int f = 0; f < FT; ++f) wbuf[kk % PFO][f] = nxt[f];
         }
     }
 
     // ---- Y (+ bias), rounded once; rows past L are dropped -------------------------
-    const rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + b * a.ysb, (uint32_t)(((L - 1) * a.yss + E) * 2));
     const T* const bo = static_cast<const T*>(a.bias[3]);
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
