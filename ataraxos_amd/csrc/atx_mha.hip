@@ -15,10 +15,10 @@
 //
 // Per head h (8 waves):
 //  A. [Q_h | K_h | V_h]^T = W_h X^T: 12 feature tiles x NP position tiles,
-//     K = E.  Wave w owns feature tiles 3 (w % 4) .. +2 and half of the
-//     position tiles; the weight operand streams from memory (16-byte loads,
-//     prefetched a few k-steps ahead), X from LDS.  Results are rounded to the
-//     16-bit type (where nn.Linear rounds them) and stored row-major.
+//     K = E, on waves 0..3 (feature tiles 3w .. 3w+2, every position): the
+//     weight operand streams from L2 once per sample (16-byte loads, the next
+//     k-step in flight), X from LDS.  Results are rounded to the 16-bit type
+//     (where nn.Linear rounds them) and stored row-major.
 //  B. Attention, one 16-query tile per wave, as the attention kernel does
 //     it: S^T = K Q^T, row softmax in registers, O^T = V^T P^T with V^T from
 //     transposing LDS reads; O is rounded and stored to y.
@@ -47,10 +47,14 @@ struct MhaArgs {
 
 namespace {
 
-constexpr int kThreads = 512;
+#ifndef ATX_MHA_WAVES
+#define ATX_MHA_WAVES 8
+#endif
+constexpr int kWaves = ATX_MHA_WAVES;  // per workgroup (one workgroup per CU)
+constexpr int kThreads = kWaves * 64;
 constexpr int kD = 64;  // head_dim
 #ifndef ATX_MHA_PREFETCH
-#define ATX_MHA_PREFETCH 2
+#define ATX_MHA_PREFETCH 1
 #endif
 constexpr int PFD = ATX_MHA_PREFETCH;  // k-steps of weight loads in flight ahead of the MFMAs
 
@@ -87,16 +91,17 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
     constexpr int NKC = (NP + 1) / 2;  // 32-key chunks
     constexpr int LV = NKC * 32;       // V rows staged
     constexpr int KS = E / 32;         // k-steps of a projection
-    constexpr int PH = (NP + 1) / 2;   // position tiles of a wave in phase A
-    constexpr int FT = H / 2;          // output feature tiles of a wave in phase C
+    constexpr int FT = H / 2;                      // output feature tiles of a wave (8 groups)
+    constexpr int NPGO = kWaves / 8;               // position groups in the output projection
+    constexpr int PO = (NP + NPGO - 1) / NPGO;     // position tiles of a wave there
     constexpr int PF = KS < PFD ? KS : PFD;  // weight prefetch depth (k-steps)
     constexpr int XC = E / 8;          // 16-byte chunks per X row
     static_assert(H % 2 == 0 && H <= 8, "H even, at most 8");
 
-    lds_t* const sx = lds_base();
-    lds_t* const sq = sx + LP * E * 2;  // Q_h, then O_h
-    lds_t* const sk = sq + LP * kD * 2;
-    lds_t* const sv = sk + LP * kD * 2;
+    lds_t* const sx0 = lds_base();
+    lds_t* const sq0 = sx0 + LP * E * 2;  // Q_h
+    lds_t* const sk0 = sq0 + LP * kD * 2;
+    lds_t* const sv0 = sk0 + LP * kD * 2;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -122,10 +127,10 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
         for (int u = 0; u < U; ++u) {
             const int idx = u * kThreads + tid;
             const int r = idx / XC, c = idx - (idx / XC) * XC;
-            if (idx < N) lds_st16(sx + eoff<E>(r, c), v[u]);
+            if (idx < N) lds_st16(sx0 + eoff<E>(r, c), v[u]);
         }
         for (int idx = tid; idx < (LV - LP) * 8; idx += kThreads)
-            lds_st16(sv + LP * kD * 2 + idx * 16, u32x4{0, 0, 0, 0});
+            lds_st16(sv0 + LP * kD * 2 + idx * 16, u32x4{0, 0, 0, 0});
     }
 
     const rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + b * a.ysb, (uint32_t)(((L - 1) * a.yss + E) * 2));
@@ -135,14 +140,6 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
     for (int i = 0; i < 4; ++i) rw[i] = make_rsrc(a.w[i], (uint32_t)(E * E * 2));
 
     // Phase A roles.
-    const int fg = wave & 3, pg = wave >> 2;
-    // Phase A position tiles p0 .. p0 + PH - 1; with NP odd the second group's
-    // last tile repeats tile NP - 1 (computed, never stored) so that the
-    // MFMA loop has no per-tile tests.
-    const int p0 = pg * PH;
-    int xpos[PH];
-#pragma unroll
-    for (int p = 0; p < PH; ++p) xpos[p] = min(p0 + p, NP - 1) * 16 * E * 2;
     // Transposing-read offsets into V (rows 4g + t, elements a4*16 + 4dt).
     int troff[4];
 #pragma unroll
@@ -158,74 +155,76 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
     __syncthreads();
 
     for (int h = 0; h < H; ++h) {
-        // ---- A: [Q_h | K_h | V_h]^T for feature tiles 3fg .. 3fg+2 ------------
+        // LDS bases re-derived per head through an opaque copy: otherwise the
+        // compiler hoists every per-tile address of both phases out of the
+        // head loop and runs out of registers.
+        lds_t* const sx = lds_opaque(sx0);
+        lds_t* const sq = lds_opaque(sq0);
+        lds_t* const sk = lds_opaque(sk0);
+        lds_t* const sv = lds_opaque(sv0);
+        // ---- A: [Q_h | K_h | V_h]^T on waves 0..3, feature tiles 3w .. 3w+2 --------
+        // Each of those waves covers every position, so each weight element is
+        // loaded once per sample (the L2 -> CU weight stream is what bounds
+        // this phase); waves 4..7 only take part in the barriers.
         {
-            f32x4 acc[3][PH];
-#pragma unroll
-            for (int f = 0; f < 3; ++f)
-#pragma unroll
-                for (int p = 0; p < PH; ++p) acc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
-            // feature tile ft = 3fg + f: matrix ft / 4, weight row h*64 + (ft % 4)*16 + m
-            rsrc_t wr[3];
-            uint32_t wrow[3];
-#pragma unroll
-            for (int f = 0; f < 3; ++f) {
-                const int ft = 3 * fg + f;
-                wr[f] = (ft >> 2) == 0 ? rw[0] : ((ft >> 2) == 1 ? rw[1] : rw[2]);
-                wrow[f] = (uint32_t)((h * kD + (ft & 3) * 16 + m) * E + 8 * g) * 2;
-            }
-            // Weight k-steps stay PF ahead of the MFMAs: each iteration issues
-            // step kk + PF first, and a scheduling barrier keeps the compiler
-            // from sinking those loads next to their use.
-            u32x4 wbuf[PF][3];
-#pragma unroll
-            for (int s2 = 0; s2 < PF; ++s2)
-#pragma unroll
-                for (int f = 0; f < 3; ++f) wbuf[s2][f] = buf_ld16_keep(wr[f], wrow[f] + s2 * 64);
-#pragma unroll
-            for (int kk = 0; kk < KS; ++kk) {
-                u32x4 wa[3], nxt[3];
-#pragma unroll
-                for (int f = 0; f < 3; ++f) {
-                    wa[f] = wbuf[kk % PF][f];
-                    if (kk + PF < KS) nxt[f] = buf_ld16_keep(wr[f], wrow[f] + (kk + PF) * 64);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                u32x4 xb[PH];
-#pragma unroll
-                for (int p = 0; p < PH; ++p) xb[p] = lds_ld16(sx + xlane[kk & 3] + xpos[p] + (kk >> 2) * 256);
+            f32x4 acc[3][NP];
+            if (wave < 4) {
 #pragma unroll
                 for (int f = 0; f < 3; ++f)
 #pragma unroll
-                    for (int p = 0; p < PH; ++p) acc[f][p] = M::mma(wa[f], xb[p], acc[f][p]);
-                if (kk + PF < KS)
+                    for (int p = 0; p < NP; ++p) acc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
+                // feature tile ft = 3w + f: matrix ft / 4, weight row h*64 + (ft % 4)*16 + m
+                rsrc_t wr[3];
+                uint32_t wrow[3];
 #pragma unroll
-                    for (int f = 0; f < 3; ++f) wbuf[kk % PF][f] = nxt[f];
-            }
-            // bias of the 4 features 4g .. 4g+3 of each tile
-            f32x4 bv[3];
+                for (int f = 0; f < 3; ++f) {
+                    const int ft = 3 * wave + f;
+                    wr[f] = (ft >> 2) == 0 ? rw[0] : ((ft >> 2) == 1 ? rw[1] : rw[2]);
+                    wrow[f] = (uint32_t)((h * kD + (ft & 3) * 16 + m) * E + 8 * g) * 2;
+                }
+                // the next k-step's weights are issued before this step's MFMAs;
+                // a scheduling barrier keeps the compiler from sinking them
+                u32x4 cur[3];
 #pragma unroll
-            for (int f = 0; f < 3; ++f) {
-                bv[f] = f32x4{0.f, 0.f, 0.f, 0.f};
-                const int ft = 3 * fg + f;
-                const T* bp = static_cast<const T*>(a.bias[ft >> 2]);
-                if (bp) {
-                    const int feat = h * kD + (ft & 3) * 16 + 4 * g;
+                for (int f = 0; f < 3; ++f) cur[f] = buf_ld16_keep(wr[f], wrow[f]);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) bv[f][i] = static_cast<float>(bp[feat + i]);
+                for (int kk = 0; kk < KS; ++kk) {
+                    u32x4 nxt[3];
+                    if (kk + 1 < KS)
+#pragma unroll
+                        for (int f = 0; f < 3; ++f) nxt[f] = buf_ld16_keep(wr[f], wrow[f] + (kk + 1) * 64);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int p = 0; p < NP; ++p) {
+                        const u32x4 xb = lds_ld16(sx + xlane[kk & 3] + p * 16 * E * 2 + (kk >> 2) * 256);
+#pragma unroll
+                        for (int f = 0; f < 3; ++f) acc[f][p] = M::mma(cur[f], xb, acc[f][p]);
+                    }
+                    if (kk + 1 < KS)
+#pragma unroll
+                        for (int f = 0; f < 3; ++f) cur[f] = nxt[f];
                 }
             }
             __syncthreads();  // every wave is done with the previous head's Q, K, V
+            if (wave < 4) {
 #pragma unroll
-            for (int f = 0; f < 3; ++f) {
-                const int ft = 3 * fg + f;
-                lds_t* const dst = ft < 4 ? sq : (ft < 8 ? sk : sv);
+                for (int f = 0; f < 3; ++f) {
+                    const int ft = 3 * wave + f;
+                    // bias of the 4 features 4g .. 4g+3 of the tile
+                    f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};
+                    const T* bp = static_cast<const T*>(a.bias[ft >> 2]);
+                    if (bp) {
+                        const int feat = h * kD + (ft & 3) * 16 + 4 * g;
 #pragma unroll
-                for (int p = 0; p < PH; ++p)
-                    if (p0 + p < NP)
-                        lds_st8(dst + xquad<kD>((p0 + p) * 16 + m, (ft & 3) * 16 + 4 * g),
-                                u32x2{M::pack2(acc[f][p][0] + bv[f][0], acc[f][p][1] + bv[f][1]),
-                                      M::pack2(acc[f][p][2] + bv[f][2], acc[f][p][3] + bv[f][3])});
+                        for (int i = 0; i < 4; ++i) bv[i] = static_cast<float>(bp[feat + i]);
+                    }
+                    lds_t* const dst = ft < 4 ? sq : (ft < 8 ? sk : sv);
+#pragma unroll
+                    for (int p = 0; p < NP; ++p)
+                        lds_st8(dst + xquad<kD>(p * 16 + m, (ft & 3) * 16 + 4 * g),
+                                u32x2{M::pack2(acc[f][p][0] + bv[0], acc[f][p][1] + bv[1]),
+                                      M::pack2(acc[f][p][2] + bv[2], acc[f][p][3] + bv[3])});
+                }
             }
         }
         __syncthreads();
@@ -339,21 +338,26 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
         for (int u = 0; u < U; ++u) {
             const int idx = u * kThreads + tid;
             const int r = idx / XC, c = idx - (idx / XC) * XC;
-            if (idx < N) lds_st16(sx + eoff<E>(r, c), v[u]);
+            if (idx < N) lds_st16(sx0 + eoff<E>(r, c), v[u]);
         }
     }
     __syncthreads();
 
-    // ---- Y^T = Wo O^T: wave w owns feature tiles FT w .. FT w + FT-1 -----------------
-    f32x4 yacc[FT][NP];
+    // ---- Y^T = Wo O^T: feature tiles FT fo .. FT fo + FT-1 of position tiles
+    // po0 .. po0 + PO - 1 (fo = wave % 8; extra tiles repeat NP - 1, unstored)
+    const int fo = wave & 7, po0 = (wave >> 3) * PO;
+    f32x4 yacc[FT][PO];
 #pragma unroll
     for (int f = 0; f < FT; ++f)
 #pragma unroll
-        for (int p = 0; p < NP; ++p) yacc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int p = 0; p < PO; ++p) yacc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
     {
+        int opos[PO];
+#pragma unroll
+        for (int p = 0; p < PO; ++p) opos[p] = min(po0 + p, NP - 1) * 16 * E * 2;
         uint32_t orow[FT];
 #pragma unroll
-        for (int f = 0; f < FT; ++f) orow[f] = (uint32_t)(((wave * FT + f) * 16 + m) * E) * 2;
+        for (int f = 0; f < FT; ++f) orow[f] = (uint32_t)(((fo * FT + f) * 16 + m) * E) * 2;
         constexpr int PFO = KS < PFD ? KS : PFD;
         u32x4 wbuf[PFO][FT];
 #pragma unroll
@@ -370,8 +374,8 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                const u32x4 ob = lds_ld16(sx + xlane[kk & 3] + p * 16 * E * 2 + (kk >> 2) * 256);
+            for (int p = 0; p < PO; ++p) {
+                const u32x4 ob = lds_ld16(sx0 + xlane[kk & 3] + opos[p] + (kk >> 2) * 256);
 #pragma unroll
                 for (int f = 0; f < FT; ++f) yacc[f][p] = M::mma(wa[f], ob, yacc[f][p]);
             }
@@ -385,14 +389,15 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
     const T* const bo = static_cast<const T*>(a.bias[3]);
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
-        const int feat = (wave * FT + f) * 16 + 4 * g;
+        const int feat = (fo * FT + f) * 16 + 4 * g;
         f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};
         if (bo)
 #pragma unroll
             for (int i = 0; i < 4; ++i) bv[i] = static_cast<float>(bo[feat + i]);
 #pragma unroll
-        for (int p = 0; p < NP; ++p)
-            buf_st8_cached(ry, (uint32_t)((p * 16 + m) * a.yss + feat) * 2,
+        for (int p = 0; p < PO; ++p)
+            if (po0 + p < NP)
+                buf_st8_cached(ry, (uint32_t)(((po0 + p) * 16 + m) * a.yss + feat) * 2,
                            u32x2{M::pack2(yacc[f][p][0] + bv[0], yacc[f][p][1] + bv[1]),
                                  M::pack2(yacc[f][p][2] + bv[2], yacc[f][p][3] + bv[3])});
     }
