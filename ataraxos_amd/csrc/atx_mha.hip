@@ -15,10 +15,10 @@
 //
 // Per head h (8 waves):
 //  A. [Q_h | K_h | V_h]^T = W_h X^T: 12 feature tiles x NP position tiles,
-//     K = E, on waves 0..3 (feature tiles 3w .. 3w+2, every position): the
-//     weight operand streams from L2 once per sample (16-byte loads, the next
-//     k-step in flight), X from LDS.  Results are rounded to the 16-bit type
-//     (where nn.Linear rounds them) and stored row-major.
+//     K = E; each wave owns whole feature tiles (2 or 1) for every position,
+//     so the weight operand streams from L2 once per sample (16-byte loads,
+//     the next k-step in flight), X from LDS.  Results are rounded to the
+//     16-bit type (where nn.Linear rounds them) and stored row-major.
 //  B. Attention, one 16-query tile per wave, as the attention kernel does
 //     it: S^T = K Q^T, row softmax in registers, O^T = V^T P^T with V^T from
 //     transposing LDS reads; O is rounded and stored to y.
@@ -80,6 +80,72 @@ __device__ inline int eoff(int r, int c) {
 inline size_t mha_lds_bytes(int E, int np) {
     const int lp = 16 * np, lv = 32 * ((np + 1) / 2);
     return (size_t)lp * E * 2 + (size_t)(2 * lp + lv) * kD * 2;
+}
+
+// [Q_h | K_h | V_h]^T feature tiles ft0 .. ft0 + NF - 1 (of 12: Q 0-3, K 4-7,
+// V 8-11) for every position tile: X^T rows from LDS, the weight rows from
+// memory with the next k-step in flight.  Results (+ bias) are rounded and
+// stored row-major into sq / sk / sv after a workgroup barrier (all waves
+// call this once per head).
+template <typename T, int E, int NP, int NF>
+__device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* sk, lds_t* sv, const int (&xlane)[4],
+                                             rsrc_t rq, rsrc_t rk, rsrc_t rv, const void* const (&bias)[4], int h,
+                                             int ft0, int m, int g) {
+    using M = Mfma16<T>;
+    constexpr int KS = E / 32;
+    f32x4 acc[NF][NP];
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) acc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
+    rsrc_t wr[NF];
+    uint32_t wrow[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        const int ft = ft0 + f;
+        wr[f] = (ft >> 2) == 0 ? rq : ((ft >> 2) == 1 ? rk : rv);
+        wrow[f] = (uint32_t)((h * kD + (ft & 3) * 16 + m) * E + 8 * g) * 2;
+    }
+    // the next k-step's weights are issued before this step's MFMAs; a
+    // scheduling barrier keeps the compiler from sinking them to their use
+    u32x4 cur[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) cur[f] = buf_ld16_keep(wr[f], wrow[f]);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+        u32x4 nxt[NF];
+        if (kk + 1 < KS)
+#pragma unroll
+            for (int f = 0; f < NF; ++f) nxt[f] = buf_ld16_keep(wr[f], wrow[f] + (kk + 1) * 64);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const u32x4 xb = lds_ld16(sx + xlane[kk & 3] + p * 16 * E * 2 + (kk >> 2) * 256);
+#pragma unroll
+            for (int f = 0; f < NF; ++f) acc[f][p] = M::mma(cur[f], xb, acc[f][p]);
+        }
+        if (kk + 1 < KS)
+#pragma unroll
+            for (int f = 0; f < NF; ++f) cur[f] = nxt[f];
+    }
+    __syncthreads();  // every wave is done with the previous head's Q, K, V
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        const int ft = ft0 + f;
+        f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};  // bias of features 4g .. 4g+3 of the tile
+        const T* bp = static_cast<const T*>(bias[ft >> 2]);
+        if (bp) {
+            const int feat = h * kD + (ft & 3) * 16 + 4 * g;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bv[i] = static_cast<float>(bp[feat + i]);
+        }
+        lds_t* const dst = ft < 4 ? sq : (ft < 8 ? sk : sv);
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+            lds_st8(dst + xquad<kD>(p * 16 + m, (ft & 3) * 16 + 4 * g),
+                    u32x2{M::pack2(acc[f][p][0] + bv[0], acc[f][p][1] + bv[1]),
+                          M::pack2(acc[f][p][2] + bv[2], acc[f][p][3] + bv[3])});
+    }
 }
 
 // H heads (even), NP 16-row position tiles (L <= 16 NP).
@@ -162,71 +228,14 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
         lds_t* const sq = lds_opaque(sq0);
         lds_t* const sk = lds_opaque(sk0);
         lds_t* const sv = lds_opaque(sv0);
-        // ---- A: [Q_h | K_h | V_h]^T on waves 0..3, feature tiles 3w .. 3w+2 --------
-        // Each of those waves covers every position, so each weight element is
-        // loaded once per sample (the L2 -> CU weight stream is what bounds
-        // this phase); waves 4..7 only take part in the barriers.
-        {
-            f32x4 acc[3][NP];
-            if (wave < 4) {
-#pragma unroll
-                for (int f = 0; f < 3; ++f)
-#pragma unroll
-                    for (int p = 0; p < NP; ++p) acc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
-                // feature tile ft = 3w + f: matrix ft / 4, weight row h*64 + (ft % 4)*16 + m
-                rsrc_t wr[3];
-                uint32_t wrow[3];
-#pragma unroll
-                for (int f = 0; f < 3; ++f) {
-                    const int ft = 3 * wave + f;
-                    wr[f] = (ft >> 2) == 0 ? rw[0] : ((ft >> 2) == 1 ? rw[1] : rw[2]);
-                    wrow[f] = (uint32_t)((h * kD + (ft & 3) * 16 + m) * E + 8 * g) * 2;
-                }
-                // the next k-step's weights are issued before this step's MFMAs;
-                // a scheduling barrier keeps the compiler from sinking them
-                u32x4 cur[3];
-#pragma unroll
-                for (int f = 0; f < 3; ++f) cur[f] = buf_ld16_keep(wr[f], wrow[f]);
-#pragma unroll
-                for (int kk = 0; kk < KS; ++kk) {
-                    u32x4 nxt[3];
-                    if (kk + 1 < KS)
-#pragma unroll
-                        for (int f = 0; f < 3; ++f) nxt[f] = buf_ld16_keep(wr[f], wrow[f] + (kk + 1) * 64);
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int p = 0; p < NP; ++p) {
-                        const u32x4 xb = lds_ld16(sx + xlane[kk & 3] + p * 16 * E * 2 + (kk >> 2) * 256);
-#pragma unroll
-                        for (int f = 0; f < 3; ++f) acc[f][p] = M::mma(cur[f], xb, acc[f][p]);
-                    }
-                    if (kk + 1 < KS)
-#pragma unroll
-                        for (int f = 0; f < 3; ++f) cur[f] = nxt[f];
-                }
-            }
-            __syncthreads();  // every wave is done with the previous head's Q, K, V
-            if (wave < 4) {
-#pragma unroll
-                for (int f = 0; f < 3; ++f) {
-                    const int ft = 3 * wave + f;
-                    // bias of the 4 features 4g .. 4g+3 of the tile
-                    f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};
-                    const T* bp = static_cast<const T*>(a.bias[ft >> 2]);
-                    if (bp) {
-                        const int feat = h * kD + (ft & 3) * 16 + 4 * g;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) bv[i] = static_cast<float>(bp[feat + i]);
-                    }
-                    lds_t* const dst = ft < 4 ? sq : (ft < 8 ? sk : sv);
-#pragma unroll
-                    for (int p = 0; p < NP; ++p)
-                        lds_st8(dst + xquad<kD>(p * 16 + m, (ft & 3) * 16 + 4 * g),
-                                u32x2{M::pack2(acc[f][p][0] + bv[0], acc[f][p][1] + bv[1]),
-                                      M::pack2(acc[f][p][2] + bv[2], acc[f][p][3] + bv[3])});
-                }
-            }
-        }
+        // ---- A: [Q_h | K_h | V_h]^T: waves 0..3 own feature tiles 2w, 2w+1
+        // (Q, K), waves 4..7 tile 4 + w (V), each for every position, so every
+        // weight element crosses from L2 once per sample and each SIMD holds
+        // one 2-tile and one 1-tile wave.
+        if (wave < 4)
+            project_head<T, E, NP, 2>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, 2 * wave, m, g);
+        else
+            project_head<T, E, NP, 1>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, 4 + wave, m, g);
         __syncthreads();
 
         // ---- B: attention of head h, one query tile per wave -------------------
