@@ -17,6 +17,11 @@ Backends (``backend`` property, the slot of attention.py:122-146):
 * ``"hip"``  — tensors on a GPU: the fused HIP kernel (``ops.attention``).
   Its range is head_dim a multiple of 16 up to 128 and at most 256 keys;
   outside that the forward raises instead of switching to another path.
+  Self-attention without autograd (inference, self-play) with head_dim 64,
+  2/4/6/8 heads, no GQA, 16-bit and up to 128 positions runs the whole layer
+  -- projections, attention, output projection -- as one launch
+  (``ops.mha_forward``); with autograd the projections stay ``nn.Linear``
+  and the attention kernel's backward applies.
 * ``"math"`` — tensors on the CPU, or training with ``dropout > 0`` (the
   kernel has no dropout, as the reference's FA3 backend has none:
   attention.py:134-138).  It keeps the semantics of attention.py:281-316.
@@ -96,6 +101,10 @@ class MultiHeadAttention(nn.Module):
         self.head_dim: int = embed_dim // num_heads
         self.dropout: float = dropout
         self.causal: bool = causal
+        # Not in the reference: False keeps the unfused GPU path (nn.Linear
+        # projections + the attention kernel) also where the one-launch
+        # layer would apply.  Not part of the state_dict.
+        self.fuse_layer: bool = True
 
         kv_dim = kv_heads * self.head_dim
         self.q_proj = nn.Linear(embed_dim, num_heads * self.head_dim, bias=qkv_bias)
@@ -116,6 +125,8 @@ class MultiHeadAttention(nn.Module):
     def forward(self, x: torch.Tensor, key_value: torch.Tensor | None = None) -> torch.Tensor:
         """``x`` ``[B, S_q, E]``; ``key_value`` ``[B, S_kv, E]`` or None -> ``[B, S_q, E]``."""
         batch, seq_q, _ = x.shape
+        if key_value is None and self._fused_ok(x):
+            return self._forward_fused(x)
         src = x if key_value is None else key_value
         q = self.q_proj(x).view(batch, seq_q, self.num_heads, self.head_dim)
         k = self.k_proj(src)
@@ -129,6 +140,24 @@ class MultiHeadAttention(nn.Module):
         else:
             attn = self._forward_math(q, k, v, is_causal)
         return cast(torch.Tensor, self.out_proj(attn.reshape(batch, seq_q, self.embed_dim)))
+
+    def _fused_ok(self, x: torch.Tensor) -> bool:
+        """The one-launch layer applies: GPU, no autograd, no dropout to run,
+        and a shape the fused kernel covers."""
+        if not self.fuse_layer or self.backend != "hip" or self.num_kv_heads != self.num_heads or self.head_dim != 64:
+            return False
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return False
+        w = self.q_proj.weight
+        return x.dtype == w.dtype and ops.mha_forward_supported(self.embed_dim, self.num_heads, x.shape[1], x.dtype)
+
+    def _forward_fused(self, x: torch.Tensor) -> torch.Tensor:
+        """Projections + attention + output projection in one kernel launch."""
+        return ops.mha_forward(
+            x, self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.out_proj.weight,
+            num_heads=self.num_heads, b_q=self.q_proj.bias, b_k=self.k_proj.bias, b_v=self.v_proj.bias,
+            b_o=self.out_proj.bias, causal=self.causal, scale=1.0 / math.sqrt(self.head_dim),
+        )
 
     def _expand_kv_heads(self, k: torch.Tensor, v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """Repeat ``(B, H_kv, S, D)`` KV heads up to ``H`` (attention.py:210-220)."""

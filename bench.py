@@ -18,8 +18,10 @@ roofline = 18.2 M samples/s).  Also reported on the same line:
   from the committed rocprofv3 counter summary when present;
 * ``mfma``: the same kernel's algorithmic FLOP rate (B x 15.36 MFLOP) against
   the 2.5 PFLOP/s dense bf16 peak;
-* ``e2e``: the full MultiHeadAttention forward of the 8 layers (QKV
-  projections, attention, output projection, residual);
+* ``e2e``: the full MultiHeadAttention forward of the 8 layers plus the
+  residual, as the module runs it in inference (one launch of the fused layer
+  kernel per layer), with its MFMA rate (B x 133.3 MFLOP per layer), and the
+  same with the unfused path (hipBLASLt projections + attention kernel);
 * ``kq_policy``: the fused key-query policy kernel at config C2;
 * ``belief_attention``: the attention kernel at the config C4 shapes
   (encoder self, decoder causal self, decoder cross with key padding);
@@ -140,12 +142,16 @@ def time_attention(torch, ops, layers, heads, head_dim, steps, warmup):
     return total_ms / steps, sum(per_launch) / len(per_launch), min(per_launch)
 
 
-def time_e2e(torch, batch, seq, embed, heads, layers_n, steps, warmup, dev):
-    """Full MHA forward (projections + fused attention + out_proj + residual) x layers."""
+def time_e2e(torch, batch, seq, embed, heads, layers_n, steps, warmup, dev, fuse=True):
+    """Full MHA forward x layers (x = x + mha(x)): with ``fuse`` each layer is
+    one launch of the fused layer kernel; without, hipBLASLt projections +
+    the attention kernel + hipBLASLt output projection."""
     from ataraxos_amd import MultiHeadAttention
 
     torch.manual_seed(45)
     mods = [MultiHeadAttention(embed, heads).to(dev, torch.bfloat16).eval() for _ in range(layers_n)]
+    for m in mods:
+        m.fuse_layer = fuse
     for m in mods:
         for p in m.parameters():
             torch.nn.init.normal_(p, std=0.02)
@@ -440,12 +446,17 @@ def main() -> int:
         },
     }
     if not args.no_extras:
-        e2e_ms = time_e2e(torch, batch, seq, embed, heads, args.layers, max(5, args.steps // 5), 3, dev)
+        e2e_ms = time_e2e(torch, batch, seq, embed, heads, args.layers, max(5, args.steps // 5), 3, dev, fuse=True)
+        unf_ms = time_e2e(torch, batch, seq, embed, heads, args.layers, max(5, args.steps // 5), 3, dev, fuse=False)
+        layer_flops = batch * (4 * 2 * seq * embed * embed + heads * 2 * 2 * seq * seq * (embed // heads))
         result["e2e"] = {
-            "what": "MultiHeadAttention forward x8 (QKV + out projections on hipBLASLt, fused HIP attention, residual)",
+            "what": "MultiHeadAttention forward x8 + residual, each layer one launch of the fused layer kernel",
             "ms_per_step": e2e_ms,
             "samples_per_s": batch / (e2e_ms * 1e-3),
-            "attention_share": (ms_step / e2e_ms) if e2e_ms > 0 else None,
+            "mfma_tflops": args.layers * layer_flops / (e2e_ms * 1e-3) / 1e12,
+            "mfma_frac": args.layers * layer_flops / (e2e_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+            "unfused_ms_per_step": unf_ms,
+            "unfused_what": "QKV + out projections on hipBLASLt, the attention kernel, residual",
         }
         result["kq_policy"] = time_kq(torch, ops, batch, dev, args.steps, args.warmup)
         result["belief_attention"] = time_belief(torch, ops, dev, args.steps, args.warmup)

@@ -118,10 +118,28 @@ def test_matches_the_unfused_module_path(cuda):
     m = MultiHeadAttention(384, 6).to(cuda, torch.bfloat16).eval()
     x = randn((16, 100, 384), 70, torch.bfloat16).to(cuda)
     with torch.no_grad():
+        m.fuse_layer = False
         unfused = m(x)
-        fused = ops.mha_forward(x, m.q_proj.weight, m.k_proj.weight, m.v_proj.weight, m.out_proj.weight, num_heads=6)
+        m.fuse_layer = True
+        fused = m(x)  # the module's inference path is the one-launch layer
+        direct = ops.mha_forward(x, m.q_proj.weight, m.k_proj.weight, m.v_proj.weight, m.out_proj.weight, num_heads=6)
+    assert torch.equal(fused, direct)
     err = (fused.float() - unfused.float()).abs().max().item()
     assert err <= 2e-2 * unfused.float().abs().max().item(), err
+
+
+def test_module_with_autograd_keeps_the_unfused_path(cuda):
+    """With autograd the module runs projections + attention kernel (which
+    has a backward); the result matches the fused inference output."""
+    torch.manual_seed(8)
+    m = MultiHeadAttention(384, 6, causal=True).to(cuda, torch.bfloat16)
+    x = randn((4, 40, 384), 71, torch.bfloat16).to(cuda).requires_grad_(True)
+    y = m(x)
+    y.float().sum().backward()
+    assert x.grad is not None and torch.isfinite(x.grad).all()
+    with torch.no_grad():
+        yf = m(x)
+    assert (y.detach().float() - yf.float()).abs().max().item() <= 2e-2 * yf.float().abs().max().item()
 
 
 def test_deterministic(cuda):
