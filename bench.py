@@ -69,27 +69,49 @@ def parse() -> argparse.Namespace:
         "--mode",
         choices=("bench", "pmc"),
         default="bench",
-        help="pmc: only launch the attention kernel `steps` times and a 1 GiB plain copy `steps` "
+        help="pmc: only launch one kernel (--pmc-kernel) `steps` times and a 1 GiB plain copy `steps` "
         "times (the calibration for rocprofv3 FETCH_SIZE / WRITE_SIZE passes); prints no JSON",
     )
+    ap.add_argument("--pmc-kernel", choices=("attn_fwd", "attn_bwd", "kq_bwd", "mha"), default="attn_fwd",
+                    help="pmc mode: the C3 attention forward, its backward, the C2 policy backward (logits) "
+                    "or the fused C3 layer")
     return ap.parse_args()
 
 
-def pmc_workload(torch, ops, batch, steps, dev) -> None:
-    """One C3 layer through the attention kernel, then a plain device copy of
-    exactly 1 GiB (read 1 GiB + write 1 GiB) to scale the byte counters."""
+def pmc_workload(torch, ops, batch, steps, dev, kernel="attn_fwd") -> None:
+    """One C3 layer through the chosen kernel `steps` times, then a plain
+    device copy of exactly 1 GiB (read 1 GiB + write 1 GiB) to scale the byte
+    counters."""
     layers = make_layers(torch, batch, 100, 384, 1, dev)
     q, k, v = (t.view(batch, 100, 6, 64) for t in layers[0])
     out = torch.empty_like(q)
-    for _ in range(steps):
-        ops.attention_forward(q, k, v, out=out)
+    if kernel == "attn_fwd":
+        for _ in range(steps):
+            ops.attention_forward(q, k, v, out=out)
+    elif kernel == "attn_bwd":
+        o = ops.attention_forward(q, k, v)
+        for _ in range(steps):
+            ops.attention_backward(q, k, v, o, o)
+    elif kernel == "kq_bwd":
+        g = torch.Generator(device=dev).manual_seed(49)
+        qk, kk = q[:, :, 0], k[:, :, 0]  # [B, 100, 64] views
+        mask = torch.rand(batch, 100, 100, generator=g, device=dev) < 0.02
+        grad = torch.randn(batch, 100 * 100, generator=g, device=dev)
+        for _ in range(steps):
+            ops.kq_policy_backward(qk, kk, grad, mask)
+    else:
+        x = layers[0][0]
+        ws = [(torch.randn(384, 384, device=dev) * 0.05).to(torch.bfloat16) for _ in range(4)]
+        y = torch.empty_like(x)
+        for _ in range(steps):
+            ops.mha_forward(x, *ws, num_heads=6, out=y)
     torch.cuda.synchronize()
     src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     for _ in range(steps):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(f"[pmc] attention x{steps} (B={batch}) and 1 GiB copy x{steps} done", file=sys.stderr, flush=True)
+    print(f"[pmc] {kernel} x{steps} (B={batch}) and 1 GiB copy x{steps} done", file=sys.stderr, flush=True)
 
 
 def make_layers(torch, batch, seq, embed, layers, dev, packed=False):
@@ -378,7 +400,7 @@ def main() -> int:
     _lib.load()
     dev = torch.device("cuda:0")
     if args.mode == "pmc":
-        pmc_workload(torch, ops, args.batch, args.steps, dev)
+        pmc_workload(torch, ops, args.batch, args.steps, dev, args.pmc_kernel)
         return 0
     batch, seq, embed, heads, head_dim = args.batch, 100, 384, 6, 64
     t0 = time.time()
