@@ -106,17 +106,23 @@ __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* 
         wr[f] = (ft >> 2) == 0 ? rq : ((ft >> 2) == 1 ? rk : rv);
         wrow[f] = (uint32_t)((h * kD + (ft & 3) * 16 + m) * E + 8 * g) * 2;
     }
-    // the next k-step's weights are issued before this step's MFMAs; a
-    // scheduling barrier keeps the compiler from sinking them to their use
-    u32x4 cur[NF];
+    // Weight k-steps stay PF ahead of the MFMAs: each iteration issues step
+    // kk + PF first, and a scheduling barrier keeps the compiler from
+    // sinking those loads to their use.
+    constexpr int PF = KS < PFD ? KS : PFD;
+    u32x4 wbuf[PF][NF];
 #pragma unroll
-    for (int f = 0; f < NF; ++f) cur[f] = buf_ld16_keep(wr[f], wrow[f]);
+    for (int s = 0; s < PF; ++s)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) wbuf[s][f] = buf_ld16_keep(wr[f], wrow[f] + s * 64);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-        u32x4 nxt[NF];
-        if (kk + 1 < KS)
+        u32x4 cur[NF], nxt[NF];
 #pragma unroll
-            for (int f = 0; f < NF; ++f) nxt[f] = buf_ld16_keep(wr[f], wrow[f] + (kk + 1) * 64);
+        for (int f = 0; f < NF; ++f) {
+            cur[f] = wbuf[kk % PF][f];
+            if (kk + PF < KS) nxt[f] = buf_ld16_keep(wr[f], wrow[f] + (kk + PF) * 64);
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
@@ -124,9 +130,9 @@ __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* 
 #pragma unroll
             for (int f = 0; f < NF; ++f) acc[f][p] = M::mma(cur[f], xb, acc[f][p]);
         }
-        if (kk + 1 < KS)
+        if (kk + PF < KS)
 #pragma unroll
-            for (int f = 0; f < NF; ++f) cur[f] = nxt[f];
+            for (int f = 0; f < NF; ++f) wbuf[kk % PF][f] = nxt[f];
     }
     __syncthreads();  // every wave is done with the previous head's Q, K, V
 #pragma unroll
