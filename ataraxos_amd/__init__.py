@@ -5,7 +5,8 @@
 * :class:`KeyQueryPolicyHead` — drop-in for the Move network's policy head,
   with the logits, legal-move mask and softmax fused on the GPU.
 * :class:`KVCache` / :func:`ops.attention_decode` — incremental causal decode;
-  :class:`SetupDecoder` runs a Setup network token by token over it.
+  :class:`SetupDecoder` runs a Setup network token by token over it and
+  :class:`BeliefDecoder` a Belief network with its encoder run once.
 * :func:`use_hip_attention` / :class:`KernelMultiheadAttention` — the Belief
   network's ``nn.TransformerDecoder`` attention through the same kernel.
 
@@ -14,7 +15,7 @@ Importing the package does not load the library or touch the GPU.
 
 from . import ops
 from .attention import MultiHeadAttention, math_attention
-from .decode import KVCache, SetupDecoder
+from .decode import BeliefDecoder, KVCache, SetupDecoder
 from .decoder import KernelMultiheadAttention, use_hip_attention
 from .policy import KeyQueryPolicyHead, masked_policy_logits, masked_policy_softmax
 
@@ -27,6 +28,7 @@ __all__ = [
     "masked_policy_softmax",
     "KVCache",
     "SetupDecoder",
+    "BeliefDecoder",
     "KernelMultiheadAttention",
     "use_hip_attention",
 ]

@@ -11,10 +11,11 @@ last row of the causal attention the reference recomputes
 from __future__ import annotations
 
 import torch
+import torch.nn.functional as F  # noqa: N812
 
 from . import ops
 
-__all__ = ["KVCache", "SetupDecoder"]
+__all__ = ["KVCache", "SetupDecoder", "BeliefDecoder"]
 
 
 class KVCache:
@@ -121,3 +122,119 @@ class SetupDecoder:
         if self.first is None:
             self.first = x
         return net.value_head(self.first), net.entropy_head(self.first), net.policy_head(x)
+
+
+class BeliefDecoder:
+    """Token-by-token decoding of a Belief network with the encoder run once.
+
+    ``net`` is the reference ``BeliefNetwork`` (``stratego/networks/belief_net.py:67-180``)
+    or any module with its structure: ``net(infostate, hidden_mask)`` returning
+    the encoder output ``[B, 100, dim]`` (:148-152), ``token_emb``,
+    ``dec_pos_emb.embed`` and ``decoder``, an ``nn.TransformerDecoder`` of
+    ``norm_first`` layers (:105-114), and ``output_proj``.
+
+    The reference's ``BeliefSampler.sample_configs``
+    (``stratego/search/belief_sampler.py:36-101``) re-runs the whole network
+    -- encoder included -- for every hidden square of every sample, one sample
+    at a time.  Here the encoder runs once for the batch, each decoder layer's
+    cross-attention keys and values are projected once from its output, the
+    self-attention keeps per-layer KV caches, and a step costs one or two
+    query rows per layer: the cross-attention through the attention kernel with the
+    key padding ``~hidden_mask`` (:159), the self-attention through
+    :func:`ops.attention_decode`.  Step t returns what the reference's full
+    decoder gives at its last position (``logits[:, -1]`` with ``t + 1``
+    tokens, belief_sampler.py:92-94); :meth:`sample` draws a whole
+    configuration for every row of the batch (the samples in parallel) with
+    the reference's placeholder convention.
+    """
+
+    def __init__(self, net: torch.nn.Module, infostate: torch.Tensor, hidden_mask: torch.Tensor,
+                 capacity: int = 40) -> None:
+        self.net = net
+        with torch.no_grad():
+            enc = net(infostate, hidden_mask)  # [B, 100, dim]: target_tokens None -> encoder output
+        self.layers = list(net.decoder.layers)
+        first = self.layers[0].self_attn
+        self.dim, self.heads = first.embed_dim, first.num_heads
+        self.head_dim = self.dim // self.heads
+        b, n, _ = enc.shape
+        self.pad = (~hidden_mask.bool()).contiguous()  # True = key ignored (memory_key_padding_mask)
+        self.memory: list[tuple[torch.Tensor, torch.Tensor]] = []
+        with torch.no_grad():
+            for layer in self.layers:
+                mha = layer.multihead_attn
+                _, w_k, w_v = mha.in_proj_weight.chunk(3)
+                b_k = b_v = None
+                if mha.in_proj_bias is not None:
+                    _, b_k, b_v = mha.in_proj_bias.chunk(3)
+                k = F.linear(enc, w_k, b_k).view(b, n, self.heads, self.head_dim)
+                v = F.linear(enc, w_v, b_v).view(b, n, self.heads, self.head_dim)
+                self.memory.append((k, v))
+        self.cache = KVCache(len(self.layers), b, self.heads, capacity, self.head_dim, dtype=enc.dtype,
+                             device=enc.device)
+        self.batch = b
+
+    def reset(self) -> None:
+        self.cache.reset()
+
+    def _row(self, pos: int, tokens: torch.Tensor) -> torch.Tensor:
+        """Run position ``pos`` with input tokens ``[B]`` through every decoder
+        layer, writing its self-attention K/V at cache row ``pos`` (attending
+        over rows 0..pos); returns the decoder output ``[B, dim]``."""
+        net, b, e = self.net, self.batch, self.dim
+        x = net.token_emb(tokens) + net.dec_pos_emb.embed[pos]
+        for li, layer in enumerate(self.layers):
+            sa = layer.self_attn
+            qkv = F.linear(layer.norm1(x), sa.in_proj_weight, sa.in_proj_bias)
+            q, k, v = (t_.reshape(b, self.heads, self.head_dim).contiguous() for t_ in qkv.chunk(3, dim=-1))
+            o = ops.attention_decode(q, self.cache.keys(li), self.cache.values(li), pos + 1, k, v)
+            x = x + sa.out_proj(o.reshape(b, e))
+            ca = layer.multihead_attn
+            w_q = ca.in_proj_weight[:e]
+            b_q = ca.in_proj_bias[:e] if ca.in_proj_bias is not None else None
+            qc = F.linear(layer.norm2(x), w_q, b_q).view(b, 1, self.heads, self.head_dim)
+            kc, vc = self.memory[li]
+            oc = ops.attention(qc, kc, vc, key_padding_mask=self.pad)
+            x = x + ca.out_proj(oc.reshape(b, e))
+            x = x + layer.linear2(layer.activation(layer.linear1(layer.norm3(x))))
+        if net.decoder.norm is not None:
+            x = net.decoder.norm(x)
+        return x
+
+    @torch.no_grad()
+    def step(self, tokens: torch.Tensor) -> torch.Tensor:
+        """Feed the token ``[B]`` (int) of the next position; returns that
+        position's logits ``[B, num_types]`` -- the last row of the full decoder
+        run over every token fed so far."""
+        if self.cache.length >= self.cache.capacity:
+            raise RuntimeError(f"BeliefDecoder: capacity {self.cache.capacity} reached")
+        x = self._row(self.cache.length, tokens)
+        self.cache.advance()
+        return self.net.output_proj(x)
+
+    @torch.no_grad()
+    def sample(self, num_tokens: int, generator: torch.Generator | None = None,
+               return_probs: bool = False) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
+        """Draw ``num_tokens`` piece types per row as the reference's sampler
+        does (belief_sampler.py:84-99): at step j the decoder input is the
+        tokens drawn so far followed by the placeholder 0, and p_j is a
+        ``multinomial`` draw from the softmax of the last position's logits.
+        Each step rewrites cache row j-1 with the drawn token and runs row j
+        with the placeholder: two query rows per layer.  Returns ``[B,
+        num_tokens]`` token indices (the reference's ``PieceType`` is index + 1)
+        and, with ``return_probs``, the step probabilities ``[B, num_tokens, types]``."""
+        if num_tokens > self.cache.capacity:
+            raise ValueError(f"BeliefDecoder.sample: {num_tokens} tokens > capacity {self.cache.capacity}")
+        self.reset()
+        zero = torch.zeros(self.batch, dtype=torch.long, device=self.pad.device)
+        toks, probs_all = [], []
+        for j in range(num_tokens):
+            if j > 0:
+                self._row(j - 1, toks[-1])  # row j-1 now holds the drawn token
+            probs = torch.softmax(self.net.output_proj(self._row(j, zero)).float(), dim=-1)
+            tok = torch.multinomial(probs, 1, generator=generator).squeeze(1)
+            toks.append(tok)
+            probs_all.append(probs)
+        self.cache.length = num_tokens
+        out = torch.stack(toks, dim=1)
+        return (out, torch.stack(probs_all, dim=1)) if return_probs else out
