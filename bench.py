@@ -32,6 +32,12 @@ roofline = 18.2 M samples/s).  Also reported on the same line:
   bounded sample of the same layer, rank 0 only.
 
 ``python bench.py --gpus N --steps K --warmup W``; only N=1 is supported.
+
+Warm-up: after an idle spell the MI355X needs about 80-100 ms of continuous
+work before a launch reaches its steady duration (a C4 encoder launch went
+from 190 us to 148 us over the first 100 ms).  The default 60 warm-up steps
+of the main leg are ~100 ms; every other leg first runs its own launches
+untimed for at least ``SETTLE_MS``.
 """
 
 from __future__ import annotations
@@ -51,13 +57,14 @@ METRIC = "Move-net attn fwd samples/s @B=4096,L=100 bf16; % of bf16 MFMA peak"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
 TRAFFIC_FILE = ROOT / "profiles" / "attn_fwd_c3_traffic.json"
+SETTLE_MS = 150.0
 
 
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=60)
     ap.add_argument("--batch", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -189,7 +196,7 @@ def time_e2e(torch, batch, seq, embed, heads, layers_n, steps, warmup, dev, fuse
     with torch.inference_mode():
         for _ in range(warmup):
             step()
-        torch.cuda.synchronize()
+        _settle(torch, step)
         a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         for _ in range(steps):
@@ -219,15 +226,34 @@ def time_kq(torch, ops, batch, dev, steps, warmup):
     }
 
 
+def _settle(torch, fn, min_ms=SETTLE_MS):
+    """Run ``fn()`` untimed, in bursts, until the GPU has been kept busy with
+    it for at least ``min_ms`` of wall time, so that what follows is timed at
+    the steady clocks."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 1
+    while True:
+        t1 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        now = time.perf_counter()
+        if (now - t0) * 1e3 >= min_ms:
+            return
+        if (now - t1) * 1e3 < 20.0:
+            n *= 2
+
+
 def _mean_launch_ms(torch, fn, steps, warmup):
     """Mean time per call of ``fn()`` (one kernel launch) over ``steps``
-    back-to-back calls, from one event pair around them.  An untimed burst
-    queued right before keeps the GPU busy (and at its working clocks) while
-    the host enqueues the timed calls, so host launch overhead of short
-    kernels does not enter the time."""
+    back-to-back calls, from one event pair around them, after ``warmup``
+    calls and :func:`_settle`.  An untimed burst queued right before keeps the
+    GPU busy while the host enqueues the timed calls, so host launch overhead
+    of short kernels does not enter the time."""
     for _ in range(warmup):
         fn()
-    torch.cuda.synchronize()
+    _settle(torch, fn)
     for _ in range(max(warmup, 20)):
         fn()
     a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -305,7 +331,7 @@ def time_decode(torch, ops, dev, reps):
                 ops.attention_decode(q, kc, vc, t, kn, vn, out=out)
 
     sequence()
-    torch.cuda.synchronize()
+    _settle(torch, sequence)
     a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(reps):
