@@ -9,6 +9,9 @@
   :class:`BeliefDecoder` a Belief network with its encoder run once.
 * :func:`use_hip_attention` / :class:`KernelMultiheadAttention` — the Belief
   network's ``nn.TransformerDecoder`` attention through the same kernel.
+* :class:`StrategoRolloutBuffer` — drop-in for the reference's CUDA self-play
+  simulator: N games on the GPU producing the legal-move masks and
+  infostates the networks consume.
 
 Importing the package does not load the library or touch the GPU.
 """
@@ -18,6 +21,7 @@ from .attention import MultiHeadAttention, math_attention
 from .decode import BeliefDecoder, KVCache, SetupDecoder
 from .decoder import KernelMultiheadAttention, use_hip_attention
 from .policy import KeyQueryPolicyHead, masked_policy_logits, masked_policy_softmax
+from .rollout import StrategoRolloutBuffer
 
 __all__ = [
     "ops",
@@ -31,4 +35,5 @@ __all__ = [
     "BeliefDecoder",
     "KernelMultiheadAttention",
     "use_hip_attention",
+    "StrategoRolloutBuffer",
 ]

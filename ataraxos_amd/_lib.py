@@ -195,7 +195,6 @@ class AtxError(RuntimeError):
         self.code = code
 
 
-# Exported symbols, as declared in include/ataraxos_attn.h.
 class AttnBwdParams(ctypes.Structure):
     _fields_ = [
         ("abi_version", _i32),
@@ -218,6 +217,26 @@ class AttnBwdParams(ctypes.Structure):
     ]
 
 
+class RolloutState(ctypes.Structure):
+    """AtxRolloutState of include/ataraxos_rollout.h: the device arrays of N
+    simulated games."""
+
+    _fields_ = [("abi_version", _i32), ("n_games", _i32)] + [
+        (name, _ptr)
+        for name in (
+            "board_owner", "board_piece", "current_player", "move_number", "moves_since_attack", "outcome",
+            "terminated", "flag_captured", "terminated_since", "moved_squares", "revealed_squares",
+            "move_history", "move_history_head", "move_history_len", "two_square_count",
+            "two_square_pair_lo", "two_square_pair_hi", "two_square_violation", "zobrist_table",
+            "chase_hashes", "chase_hash_head", "chase_hash_len", "chase_last_src", "chasing_violation",
+        )
+    ]
+
+
+_state_ptr = ctypes.POINTER(RolloutState)
+
+# Exported symbols, as declared in include/ataraxos_attn.h and
+# include/ataraxos_rollout.h.
 ENTRY_POINTS = {
     "atx_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnParams), _ptr]),
     "atx_attn_bwd": (ctypes.c_int, [ctypes.POINTER(AttnBwdParams), _ptr]),
@@ -225,6 +244,13 @@ ENTRY_POINTS = {
     "atx_kq_bwd": (ctypes.c_int, [ctypes.POINTER(KqBwdParams), _ptr]),
     "atx_mha_fwd": (ctypes.c_int, [ctypes.POINTER(MhaParams), _ptr]),
     "atx_attn_decode_fwd": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr]),
+    # include/ataraxos_rollout.h
+    "atx_rollout_apply": (ctypes.c_int, [_state_ptr, _ptr, _ptr]),
+    "atx_rollout_legal_mask": (ctypes.c_int, [_state_ptr, _ptr, _ptr]),
+    "atx_rollout_infostate": (ctypes.c_int, [_state_ptr, _ptr, _ptr]),
+    "atx_rollout_reset": (ctypes.c_int, [_state_ptr, _ptr, _ptr, _i32, _ptr]),
+    "atx_rollout_hash": (ctypes.c_int, [_state_ptr, _ptr, _ptr]),
+    "atx_rollout_hello": (ctypes.c_int, [_ptr, _i32, _ptr]),
     "atx_last_error": (ctypes.c_char_p, []),
     "atx_abi_version": (ctypes.c_int, []),
 }

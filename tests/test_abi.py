@@ -30,6 +30,7 @@ STRUCTS = {
     "AtxKqBwdParams": _lib.KqBwdParams,
     "AtxMhaParams": _lib.MhaParams,
     "AtxDecodeParams": _lib.DecodeParams,
+    "AtxRolloutState": _lib.RolloutState,
 }
 
 
@@ -66,7 +67,8 @@ def test_header_constants_match_bindings():
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
 def test_struct_layouts_match_c_compiler(tmp_path):
-    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "ataraxos_attn.h"', "int main(void) {"]
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "ataraxos_attn.h"', '#include "ataraxos_rollout.h"',
+             "int main(void) {"]
     for cname, py in STRUCTS.items():
         lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
         for fname, _ in py._fields_:
@@ -295,3 +297,29 @@ def test_missing_library_raises_loudly(monkeypatch, tmp_path):
     with pytest.raises(_lib.AtxError, match="not found"):
         _lib.load()
     assert not _lib.available()
+
+
+def test_rollout_validation_codes():
+    """atx_rollout_*: ABI mismatch, negative and zero game counts, null
+    arrays; none of these reaches a launch."""
+    lib = _lib.load()
+    st = _lib.RolloutState()
+    st.abi_version = _lib.ABI_VERSION
+    st.n_games = 0
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced
+    for name, args in (("atx_rollout_apply", (fake,)), ("atx_rollout_legal_mask", (fake,)),
+                       ("atx_rollout_infostate", (fake,)), ("atx_rollout_hash", (fake,)),
+                       ("atx_rollout_reset", (fake, fake, 1))):
+        fn = getattr(lib, name)
+        assert fn(ctypes.byref(st), *args, None) == _lib.OK, name  # zero games: nothing to do
+        st.abi_version = 0
+        assert fn(ctypes.byref(st), *args, None) == _lib.ERR_ABI
+        assert "abi_version" in _lib.last_error()
+        st.abi_version, st.n_games = _lib.ABI_VERSION, -1
+        assert fn(ctypes.byref(st), *args, None) == _lib.ERR_INVALID_ARGUMENT
+        st.n_games = 4  # arrays still null
+        assert fn(ctypes.byref(st), *args, None) == _lib.ERR_INVALID_ARGUMENT
+        assert "null" in _lib.last_error()
+        st.n_games = 0
+    assert lib.atx_rollout_hello(None, -1, None) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.atx_rollout_hello(None, 0, None) == _lib.OK
