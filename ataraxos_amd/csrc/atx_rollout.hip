@@ -19,11 +19,10 @@
 //                      mask bytes is formed from 16 bits of those sets and
 //                      written once (the reference clears the mask with a
 //                      separate torch::zeros pass and then sets entries).
-//   rollout_infostate  a workgroup per (game, quarter of its 48,800 floats),
-//                      per-square codes and the last-32-moves list staged in
-//                      LDS, every output float written once with 16-byte
-//                      streaming stores (the reference: a zeroing pass plus
-//                      one thread per float).
+//   rollout_infostate  one thread per 16-byte chunk of the output, no LDS,
+//                      no barrier: every output float written once with
+//                      16-byte streaming stores (the reference: a zeroing
+//                      pass plus one thread per float).
 //   rollout_reset      one wave per game, lanes over squares and ring slots.
 //   rollout_hash       one wave per game, XOR butterfly.
 //
@@ -341,86 +340,69 @@ __global__ __launch_bounds__(kMaskThreads) void rollout_legal_mask(AtxRolloutSta
 // ---------------------------------------------------------------------------
 // infostate
 // ---------------------------------------------------------------------------
-constexpr int kInfoThreads = 256;
-constexpr int kInfoParts = 4;                              // workgroups per game
-constexpr int kInfoChunks = kChannels * kSq / 4;           // 12,200 chunks of 4 floats
-constexpr int kInfoPartChunks = kInfoChunks / kInfoParts;  // 3,050
-static_assert(kInfoChunks % kInfoParts == 0, "infostate split");
+constexpr int kInfoChunks = kChannels * kSq / 4;  // 12,200 chunks of 4 floats per game
 
-__global__ __launch_bounds__(kInfoThreads) void rollout_infostate(AtxRolloutState st, float* __restrict__ out) {
-    // per-square code: bit 0 own, 1 opponent, 2 empty, 3 revealed, 4 moved
-    __shared__ uint8_t s_code[kSq];
-    __shared__ uint8_t s_pc[kSq];
-    __shared__ int16_t s_hsrc[kHist], s_hdst[kHist];  // k-th most recent move, -1 past the length
-    const int t = threadIdx.x;
-    const int g = blockIdx.x / kInfoParts, part = blockIdx.x % kInfoParts;
-    const int me = st.current_player[g];
-    if (t < kSq) {
-        const int64_t i = (int64_t)g * kSq + t;
-        const int o = st.board_owner[i];
-        s_code[t] = (uint8_t)((o == me ? 1 : 0) | (o != me && o != kEmpty ? 2 : 0) | (o == kEmpty ? 4 : 0) |
-                              (st.revealed_squares[i] ? 8 : 0) | (st.moved_squares[i] ? 16 : 0));
-        s_pc[t] = (uint8_t)st.board_piece[i];
-    } else if (t >= 128 && t < 128 + kHist) {
-        const int k = t - 128;
-        int16_t hs = -1, hd = -1;
-        if (k < st.move_history_len[g]) {
-            const int head = st.move_history_head[g];
-            const int32_t a = st.move_history[(int64_t)g * kHist + ((head - 1 - k + 2 * kHist) & (kHist - 1))];
-            hs = (int16_t)(a / kSq);
-            hd = (int16_t)(a % kSq);
-        }
-        s_hsrc[k] = hs;
-        s_hdst[k] = hd;
-    }
-    __syncthreads();
-    const float turn = (float)st.move_number[g] / (float)kMaxGameLength;
-    const float quiet = (float)st.moves_since_attack[g] / (float)kNoAttackLimit;
-    const float uniform = 1.0f / 12.0f;
-    float* base = out + (int64_t)g * kChannels * kSq;
-    const int c_end = (part + 1) * kInfoPartChunks;
-    for (int c = part * kInfoPartChunks + t; c < c_end; c += kInfoThreads) {
-        const int ch = c / 25, s0 = (c - ch * 25) * 4;
+// One 16-byte chunk (4 squares of one channel) per thread, every thread of
+// the grid independent: 85 % of the chunks are the all-zero channels 43-455
+// and cost a store; a board channel reads its 4 squares' owner, piece,
+// revealed and moved bytes as one aligned 4-byte word each (mostly L2 hits,
+// a game's board is shared by its 1,075 board-channel chunks).
+__global__ __launch_bounds__(256) void rollout_infostate(AtxRolloutState st, float* __restrict__ out, int64_t total) {
+    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (c >= total) return;
+    const int g = (int)(c / kInfoChunks);
+    const int cl = (int)(c - (int64_t)g * kInfoChunks);
+    const int ch = cl / 25, s0 = (cl - ch * 25) * 4;
+    u32x4 u = {0u, 0u, 0u, 0u};
+    if (ch < 43) {
+        const int64_t b = (int64_t)g * kSq + s0;
+        const uint32_t ow4 = *reinterpret_cast<const uint32_t*>(st.board_owner + b);
+        const uint32_t pc4 = *reinterpret_cast<const uint32_t*>(st.board_piece + b);
+        const uint32_t rv4 = *reinterpret_cast<const uint32_t*>(st.revealed_squares + b);
+        const uint32_t mv4 = *reinterpret_cast<const uint32_t*>(st.moved_squares + b);
+        const int me = st.current_player[g];
+        const float turn = (float)st.move_number[g] / (float)kMaxGameLength;
+        const float quiet = (float)st.moves_since_attack[g] / (float)kNoAttackLimit;
         float v[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int s = s0 + j;
-            const int code = s_code[s], p = s_pc[s];
-            const bool own = code & 1, opp = code & 2, rev = code & 8, mov = code & 16;
-            float x = 0.0f;
-            if (ch < 12) {
-                x = own && p == ch + 1 ? 1.0f : 0.0f;
-            } else if (ch < 24) {
-                x = opp ? (rev ? (p == ch - 11 ? 1.0f : 0.0f) : uniform) : 0.0f;
-            } else if (ch < 36) {
-                x = own ? (rev ? (p == ch - 23 ? 1.0f : 0.0f) : uniform) : 0.0f;
-            } else if (ch == 36) {
-                x = own && !rev ? 1.0f : 0.0f;
-            } else if (ch == 37) {
-                x = opp && !rev ? 1.0f : 0.0f;
-            } else if (ch == 38) {
-                x = (code & 4) ? 1.0f : 0.0f;
-            } else if (ch == 39) {
-                x = own && mov ? 1.0f : 0.0f;
-            } else if (ch == 40) {
-                x = opp && mov ? 1.0f : 0.0f;
-            } else if (ch == 41) {
-                x = turn;
-            } else if (ch == 42) {
-                x = quiet;
-            } else if (ch >= 456) {
-                const int k = ch - 456;
-                x = s == s_hdst[k] ? 1.0f : (s == s_hsrc[k] ? -1.0f : 0.0f);
-            }
+            const int o = (int)(int8_t)(ow4 >> (8 * j)), p = (int)(int8_t)(pc4 >> (8 * j));
+            const bool rev = (rv4 >> (8 * j)) & 0xffu, mov = (mv4 >> (8 * j)) & 0xffu;
+            const bool own = o == me, opp = o != me && o != kEmpty;
+            float x;
+            if (ch < 12) x = own && p == ch + 1 ? 1.0f : 0.0f;                                   // own piece types
+            else if (ch < 24) x = opp ? (rev ? (p == ch - 11 ? 1.0f : 0.0f) : 1.0f / 12.0f) : 0.0f;  // opponent's
+            else if (ch < 36) x = own ? (rev ? (p == ch - 23 ? 1.0f : 0.0f) : 1.0f / 12.0f) : 0.0f;  // own, as seen
+            else if (ch == 36) x = own && !rev ? 1.0f : 0.0f;
+            else if (ch == 37) x = opp && !rev ? 1.0f : 0.0f;
+            else if (ch == 38) x = o == kEmpty ? 1.0f : 0.0f;
+            else if (ch == 39) x = own && mov ? 1.0f : 0.0f;
+            else if (ch == 40) x = opp && mov ? 1.0f : 0.0f;
+            else if (ch == 41) x = turn;
+            else x = quiet;
             v[j] = x;
         }
-        u32x4 u;
         u.x = __builtin_bit_cast(uint32_t, v[0]);
         u.y = __builtin_bit_cast(uint32_t, v[1]);
         u.z = __builtin_bit_cast(uint32_t, v[2]);
         u.w = __builtin_bit_cast(uint32_t, v[3]);
-        st16_stream(base + (int64_t)c * 4, u);
+    } else if (ch >= 456) {
+        // the k-th most recent move: +1 at its destination, -1 at its source
+        const int k = ch - 456;
+        if (k < st.move_history_len[g]) {
+            const int head = st.move_history_head[g];
+            const int32_t a = st.move_history[(int64_t)g * kHist + ((head - 1 - k + 2 * kHist) & (kHist - 1))];
+            const int hs = a / kSq, hd = a % kSq;
+            float v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = s0 + j == hd ? 1.0f : (s0 + j == hs ? -1.0f : 0.0f);
+            u.x = __builtin_bit_cast(uint32_t, v[0]);
+            u.y = __builtin_bit_cast(uint32_t, v[1]);
+            u.z = __builtin_bit_cast(uint32_t, v[2]);
+            u.w = __builtin_bit_cast(uint32_t, v[3]);
+        }
     }
+    st16_stream(out + c * 4, u);
 }
 
 // ---------------------------------------------------------------------------
@@ -539,10 +521,15 @@ extern "C" int atx_rollout_infostate(const AtxRolloutState* st, float* out, void
     if (st->n_games == 0) return ATX_OK;
     if (!out) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_rollout_infostate: null output");
     if (!aligned16(out)) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_rollout_infostate: output must be 16-byte aligned");
-    if ((int64_t)st->n_games * kInfoParts > 0x7fffffffLL)
-        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_rollout_infostate: %d games exceed the grid", st->n_games);
-    hipLaunchKernelGGL(rollout_infostate, dim3(st->n_games * kInfoParts), dim3(kInfoThreads), 0,
-                       static_cast<hipStream_t>(stream), *st, out);
+    const void* words[] = {st->board_owner, st->board_piece, st->revealed_squares, st->moved_squares};
+    for (const void* p : words)
+        if (reinterpret_cast<uintptr_t>(p) & 3u)
+            ATX_FAIL(ATX_ERR_INVALID_ARGUMENT,
+                     "atx_rollout_infostate: board_owner, board_piece, revealed_squares and moved_squares must be "
+                     "4-byte aligned");
+    const int64_t total = (int64_t)st->n_games * kInfoChunks;
+    hipLaunchKernelGGL(rollout_infostate, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), *st, out, total);
     ATX_CHECK_LAUNCH("atx_rollout_infostate");
     return ATX_OK;
 }

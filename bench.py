@@ -28,6 +28,8 @@ roofline = 18.2 M samples/s).  Also reported on the same line:
 * ``decode``: the KV-cache decode kernel over config C5's 4 layers x 40 steps;
 * ``backward``: the attention backward kernel (dQ, dK, dV) of one C3 layer;
 * ``kq_backward``: the policy-head backward kernel (dq, dk) at config C2;
+* ``rollout``: the self-play producer (HIP Stratego simulator) at 4096 games:
+  legal-move mask and infostate kernels against the HBM roofline, one ply;
 * ``cpu_baseline``: the reference's math path (torch on the host CPU) on a
   bounded sample of the same layer, rank 0 only.
 
@@ -70,7 +72,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--qkv", choices=("separate", "packed"), default="separate",
                     help="q/k/v as three tensors or as views of one fused [B, L, 3E] projection")
-    ap.add_argument("--no-extras", action="store_true", help="skip the e2e, kq_policy, belief_attention, decode and backward legs")
+    ap.add_argument("--no-extras", action="store_true", help="skip the e2e, kq_policy, belief_attention, decode, backward and rollout legs")
     ap.add_argument("--cpu-sample", type=int, default=1024, help="batch of the CPU baseline sample")
     ap.add_argument(
         "--mode",
@@ -389,6 +391,71 @@ def time_kq_backward(torch, ops, batch, dev, steps, warmup):
     return {"config": "C2 policy head backward, B=4096, 100x100, d=64, bf16 q/k, fp32 gradient", "legs": legs}
 
 
+def time_rollout(torch, dev, steps, warmup):
+    """The self-play producer at the config-2 batch: 4096 games of the HIP
+    Stratego simulator in mid-game positions (random full setups, 40 random
+    legal plies).  Legal-move mask and infostate kernels as bursts against
+    the HBM roofline; ``apply`` per launch (events around each launch) over
+    ``steps`` plies of random legal play, finished games restarted."""
+    from ataraxos_amd import StrategoRolloutBuffer
+
+    n = 4096
+    g = torch.Generator(device=dev).manual_seed(50)
+    counts = {1: 1, 2: 8, 3: 5, 4: 4, 5: 4, 6: 4, 7: 3, 8: 2, 9: 1, 10: 1, 11: 1, 12: 6}
+    pieces = torch.tensor([p for p, k in counts.items() for _ in range(k)], dtype=torch.int8, device=dev)
+
+    def setups():
+        red = torch.zeros(n, 10, 10, dtype=torch.int8, device=dev)
+        blue = torch.zeros_like(red)
+        for grid, rows in ((red, slice(0, 4)), (blue, slice(6, 10))):
+            perm = torch.argsort(torch.rand(n, 40, generator=g, device=dev), dim=1)
+            grid[:, rows] = pieces[perm].view(n, 4, 10)
+        return red, blue
+
+    buf = StrategoRolloutBuffer(n, 0)
+    buf.reset_all(*setups())
+    mask = torch.empty(n, 100, 100, dtype=torch.bool, device=dev)
+    info = torch.empty(n, 488, 10, 10, dtype=torch.float32, device=dev)
+
+    def pick():
+        m = buf.compute_legal_action_mask(out=mask).view(n, -1)
+        a = torch.rand(n, 10000, generator=g, device=dev).masked_fill_(~m, -1.0).argmax(dim=1)
+        return a.masked_fill_(~m.any(dim=1), -1)
+
+    for ply in range(40):
+        buf.apply_actions(pick())
+        if ply % 10 == 9:
+            buf.reset_terminated(*setups())
+    ms_mask = _mean_launch_ms(torch, lambda: buf.compute_legal_action_mask(out=mask), steps, warmup)
+    ms_info = _mean_launch_ms(torch, lambda: buf.compute_infostate_tensor(out=info), steps, warmup)
+    ms_hash = _mean_launch_ms(torch, lambda: buf.hash_board(), steps, warmup)
+    pairs = []
+    for ply in range(steps):
+        a = pick()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        buf.apply_actions(a)
+        e1.record()
+        pairs.append((e0, e1))
+        if ply % 10 == 9:
+            buf.reset_terminated(*setups())
+    torch.cuda.synchronize()
+    ms_apply = sum(a.elapsed_time(z) for a, z in pairs) / len(pairs)
+    mask_bytes = 10000 + 200 + 1  # mask written; owner, piece, side to move read
+    info_bytes = 488 * 100 * 4 + 400 + 32 * 4 + 13  # infostate written; board, flags, history, scalars read
+    legs = {
+        "legal_mask": _leg("legal-move mask [4096, 100, 100] bool", ms_mask, n * mask_bytes, n),
+        "infostate": _leg("infostate [4096, 488, 10, 10] float32", ms_info, n * info_bytes, n),
+        "apply": {"what": "apply_actions, one ply of random legal play", "kernel_us": ms_apply * 1e3,
+                  "games_per_s": n / (ms_apply * 1e-3)},
+        "hash": {"what": "Zobrist hash of every board", "kernel_us": ms_hash * 1e3},
+    }
+    step_ms = ms_mask + ms_info + ms_apply
+    return {"config": "self-play producer, 4096 games (config 2's batch), mid-game positions", "legs": legs,
+            "ply_us": step_ms * 1e3, "game_plies_per_s": n / (step_ms * 1e-3),
+            "note": "ply_us = legal mask + infostate + apply: what the producer launches per ply"}
+
+
 def cpu_baseline(sample: int) -> dict:
     from oracle.cpu_baseline import attention_baseline
 
@@ -511,6 +578,7 @@ def main() -> int:
         result["decode"] = time_decode(torch, ops, dev, max(3, args.steps // 10))
         result["backward"] = time_backward(torch, ops, batch, dev, args.steps, args.warmup)
         result["kq_backward"] = time_kq_backward(torch, ops, batch, dev, args.steps, args.warmup)
+        result["rollout"] = time_rollout(torch, dev, args.steps, args.warmup)
         print("[bench] extras timed", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_sample)

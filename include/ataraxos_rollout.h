@@ -70,7 +70,7 @@ typedef struct AtxRolloutState {
 int atx_rollout_apply(const AtxRolloutState* st, const int64_t* actions, void* stream);
 
 /*
- * mask (bool [N, 100, 100], device): mask[g, src, dst] = 1 where moving the
+ * mask (bool [N, 100, 100], device, 16-byte aligned): mask[g, src, dst] = 1 where moving the
  * side to move's piece from src to dst is legal, 0 elsewhere.  Every byte is
  * written; the caller need not clear the buffer.
  * Replaces compute_legal_action_mask (stratego_buffer.cpp:124-139) and
@@ -79,8 +79,10 @@ int atx_rollout_apply(const AtxRolloutState* st, const int64_t* actions, void* s
 int atx_rollout_legal_mask(const AtxRolloutState* st, uint8_t* mask, void* stream);
 
 /*
- * out (float32 [N, 488, 10, 10], device): the infostate from the side to
- * move's perspective; channels 43-455 are 0.  Every element is written.
+ * out (float32 [N, 488, 10, 10], device, 16-byte aligned): the infostate
+ * from the side to move's perspective; channels 43-455 are 0.  Every element
+ * is written.  board_owner, board_piece, revealed_squares and moved_squares
+ * must be 4-byte aligned (they are read four squares at a time).
  * Replaces compute_infostate_tensor (stratego_buffer.cpp:154-178) and
  * compute_infostate_kernel (stratego_buffer.cu:663-770).
  */
