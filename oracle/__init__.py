@@ -19,6 +19,14 @@ Modules (each function cites the reference file:line it restates):
   full causal recompute the reference performs (selfplay.py:139-146,181).
 * :mod:`oracle.cpu_baseline` — a torch-on-CPU port of the same math path,
   timed as the reported CPU baseline.
+* :mod:`oracle.rollout` (+ ``rollout.c``, built with gcc) — the self-play
+  simulator of csrc/stratego_buffer.cu / .cpp: apply_actions, the legal-move
+  mask, reset, the infostate and the Zobrist hash, one loop per game.  Pinned
+  by the reference's own simulator tests, whose positions and expected
+  values are known answers (tests/_rollout_scenarios.py), and by two code
+  paths that must agree: the mask against apply's validation over all 10,000
+  actions, the mask's "any move" against the no-move loss; the hash by its
+  XOR-linearity.
 
 Pinning.  The reference holds no golden values for this path (its tests check
 invariants only), so every oracle function is pinned by checks in
