@@ -81,9 +81,9 @@ def parse() -> argparse.Namespace:
         help="pmc: only launch one kernel (--pmc-kernel) `steps` times and a 1 GiB plain copy `steps` "
         "times (the calibration for rocprofv3 FETCH_SIZE / WRITE_SIZE passes); prints no JSON",
     )
-    ap.add_argument("--pmc-kernel", choices=("attn_fwd", "attn_bwd", "kq_bwd", "mha"), default="attn_fwd",
-                    help="pmc mode: the C3 attention forward, its backward, the C2 policy backward (logits) "
-                    "or the fused C3 layer")
+    ap.add_argument("--pmc-kernel", choices=("attn_fwd", "attn_bwd", "kq_bwd", "mha", "rollout"), default="attn_fwd",
+                    help="pmc mode: the C3 attention forward, its backward, the C2 policy backward (logits), "
+                    "the fused C3 layer, or the simulator's infostate + legal-mask kernels at 4096 games")
     return ap.parse_args()
 
 
@@ -91,6 +91,19 @@ def pmc_workload(torch, ops, batch, steps, dev, kernel="attn_fwd") -> None:
     """One C3 layer through the chosen kernel `steps` times, then a plain
     device copy of exactly 1 GiB (read 1 GiB + write 1 GiB) to scale the byte
     counters."""
+    if kernel == "rollout":
+        from ataraxos_amd import StrategoRolloutBuffer
+
+        buf, _ = _rollout_midgame(torch, dev, batch)
+        mask = torch.empty(batch, 100, 100, dtype=torch.bool, device=dev)
+        info = torch.empty(batch, 488, 10, 10, dtype=torch.float32, device=dev)
+        for _ in range(steps):
+            buf.compute_infostate_tensor(out=info)
+            buf.compute_legal_action_mask(out=mask)
+        _copy_calibration(torch, steps, dev)
+        print(f"[pmc] rollout infostate + mask x{steps} ({batch} games) and 1 GiB copy x{steps} done",
+              file=sys.stderr, flush=True)
+        return
     layers = make_layers(torch, batch, 100, 384, 1, dev)
     q, k, v = (t.view(batch, 100, 6, 64) for t in layers[0])
     out = torch.empty_like(q)
@@ -114,13 +127,17 @@ def pmc_workload(torch, ops, batch, steps, dev, kernel="attn_fwd") -> None:
         y = torch.empty_like(x)
         for _ in range(steps):
             ops.mha_forward(x, *ws, num_heads=6, out=y)
+    _copy_calibration(torch, steps, dev)
+    print(f"[pmc] {kernel} x{steps} (B={batch}) and 1 GiB copy x{steps} done", file=sys.stderr, flush=True)
+
+
+def _copy_calibration(torch, steps, dev) -> None:
     torch.cuda.synchronize()
     src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
     for _ in range(steps):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(f"[pmc] {kernel} x{steps} (B={batch}) and 1 GiB copy x{steps} done", file=sys.stderr, flush=True)
 
 
 def make_layers(torch, batch, seq, embed, layers, dev, packed=False):
@@ -391,15 +408,12 @@ def time_kq_backward(torch, ops, batch, dev, steps, warmup):
     return {"config": "C2 policy head backward, B=4096, 100x100, d=64, bf16 q/k, fp32 gradient", "legs": legs}
 
 
-def time_rollout(torch, dev, steps, warmup):
-    """The self-play producer at the config-2 batch: 4096 games of the HIP
-    Stratego simulator in mid-game positions (random full setups, 40 random
-    legal plies).  Legal-move mask and infostate kernels as bursts against
-    the HBM roofline; ``apply`` per launch (events around each launch) over
-    ``steps`` plies of random legal play, finished games restarted."""
+def _rollout_midgame(torch, dev, n):
+    """A simulator of ``n`` games from random full setups after 40 random
+    legal plies (finished games restarted), and its (pick, setups) helpers:
+    ``pick()`` draws one random legal action per game on the GPU."""
     from ataraxos_amd import StrategoRolloutBuffer
 
-    n = 4096
     g = torch.Generator(device=dev).manual_seed(50)
     counts = {1: 1, 2: 8, 3: 5, 4: 4, 5: 4, 6: 4, 7: 3, 8: 2, 9: 1, 10: 1, 11: 1, 12: 6}
     pieces = torch.tensor([p for p, k in counts.items() for _ in range(k)], dtype=torch.int8, device=dev)
@@ -414,11 +428,10 @@ def time_rollout(torch, dev, steps, warmup):
 
     buf = StrategoRolloutBuffer(n, 0)
     buf.reset_all(*setups())
-    mask = torch.empty(n, 100, 100, dtype=torch.bool, device=dev)
-    info = torch.empty(n, 488, 10, 10, dtype=torch.float32, device=dev)
+    scratch = torch.empty(n, 100, 100, dtype=torch.bool, device=dev)
 
     def pick():
-        m = buf.compute_legal_action_mask(out=mask).view(n, -1)
+        m = buf.compute_legal_action_mask(out=scratch).view(n, -1)
         a = torch.rand(n, 10000, generator=g, device=dev).masked_fill_(~m, -1.0).argmax(dim=1)
         return a.masked_fill_(~m.any(dim=1), -1)
 
@@ -426,6 +439,20 @@ def time_rollout(torch, dev, steps, warmup):
         buf.apply_actions(pick())
         if ply % 10 == 9:
             buf.reset_terminated(*setups())
+    return buf, (pick, setups)
+
+
+def time_rollout(torch, dev, steps, warmup):
+    """The self-play producer at the config-2 batch: 4096 games of the HIP
+    Stratego simulator in mid-game positions (random full setups, 40 random
+    legal plies).  Legal-move mask and infostate kernels as bursts against
+    the HBM roofline; ``apply`` per launch (events around each launch) over
+    ``steps`` plies of random legal play, finished games restarted."""
+    n = 4096
+    buf, play = _rollout_midgame(torch, dev, n)
+    mask = torch.empty(n, 100, 100, dtype=torch.bool, device=dev)
+    info = torch.empty(n, 488, 10, 10, dtype=torch.float32, device=dev)
+    pick, setups = play
     ms_mask = _mean_launch_ms(torch, lambda: buf.compute_legal_action_mask(out=mask), steps, warmup)
     ms_info = _mean_launch_ms(torch, lambda: buf.compute_infostate_tensor(out=info), steps, warmup)
     ms_hash = _mean_launch_ms(torch, lambda: buf.hash_board(), steps, warmup)
