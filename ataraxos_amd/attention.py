@@ -20,8 +20,9 @@ Backends (``backend`` property, the slot of attention.py:122-146):
   Self-attention without autograd (inference, self-play) with head_dim 64,
   2/4/6/8 heads, no GQA, 16-bit and up to 128 positions runs the whole layer
   -- projections, attention, output projection -- as one launch
-  (``ops.mha_forward``); with autograd the projections stay ``nn.Linear``
-  and the attention kernel's backward applies.
+  (``ops.mha_forward``) where that is faster, i.e. from the sequence length
+  :data:`FUSED_MIN_SEQ` gives for the head count; with autograd the
+  projections stay ``nn.Linear`` and the attention kernel's backward applies.
 * ``"math"`` — tensors on the CPU, or training with ``dropout > 0`` (the
   kernel has no dropout, as the reference's FA3 backend has none:
   attention.py:134-138).  It keeps the semantics of attention.py:281-316.
@@ -38,7 +39,15 @@ import torch.nn.functional as F  # noqa: N812
 
 from . import ops
 
-__all__ = ["MultiHeadAttention", "math_attention"]
+__all__ = ["MultiHeadAttention", "math_attention", "FUSED_MIN_SEQ"]
+
+# Shortest sequence at which the one-launch layer (ops.mha_forward) beats the
+# unfused path (hipBLASLt projections + the attention kernel), by head count
+# at head_dim 64, measured on MI355X at B=2048/4096 in bf16.  The fused
+# layer streams every weight from L2 once per sample whatever the length, so
+# short sequences are cheaper unfused: at 8 heads (E=512) the fused layer
+# took 967 us at L=40 against 531 us unfused, and won from L=84 on.
+FUSED_MIN_SEQ = {2: 1, 4: 64, 6: 48, 8: 84}
 
 
 def math_attention(
@@ -143,10 +152,13 @@ class MultiHeadAttention(nn.Module):
 
     def _fused_ok(self, x: torch.Tensor) -> bool:
         """The one-launch layer applies: GPU, no autograd, no dropout to run,
-        and a shape the fused kernel covers."""
+        a shape the fused kernel covers, and a sequence long enough for it to
+        beat the unfused path (:data:`FUSED_MIN_SEQ`)."""
         if not self.fuse_layer or self.backend != "hip" or self.num_kv_heads != self.num_heads or self.head_dim != 64:
             return False
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return False
+        if x.shape[1] < FUSED_MIN_SEQ.get(self.num_heads, 1 << 30):
             return False
         w = self.q_proj.weight
         return x.dtype == w.dtype and ops.mha_forward_supported(self.embed_dim, self.num_heads, x.shape[1], x.dtype)

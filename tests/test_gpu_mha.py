@@ -159,3 +159,26 @@ def test_rejects_unsupported(cuda):
     xb, wb = x.bfloat16(), w.bfloat16()
     with pytest.raises(NotImplementedError):
         ops.mha_forward(xb, wb, wb, wb, wb, num_heads=3)  # head_dim 128
+
+
+@pytest.mark.parametrize("heads,short,long", [(6, 40, 48), (8, 40, 100), (4, 48, 64)])
+def test_module_takes_the_fused_layer_only_where_it_is_faster(cuda, monkeypatch, heads, short, long):
+    """Below FUSED_MIN_SEQ the module runs the unfused path (measured faster
+    there); from it on, the one-launch layer."""
+    from ataraxos_amd import attention as attn_mod
+
+    _announce(f"mha dispatch h={heads}")
+    assert short < attn_mod.FUSED_MIN_SEQ[heads] <= long
+    calls = []
+    real = ops.mha_forward
+    monkeypatch.setattr(attn_mod.ops, "mha_forward", lambda *a, **k: calls.append(a[0].shape[1]) or real(*a, **k))
+    m = MultiHeadAttention(64 * heads, heads, causal=True).to(cuda, torch.bfloat16).eval()
+    with torch.no_grad():
+        for seq in (short, long):
+            x = randn((2, seq, 64 * heads), 90 + seq, torch.bfloat16).to(cuda)
+            m.fuse_layer = False
+            ref = m(x)
+            m.fuse_layer = True
+            got = m(x)
+            assert (got.float() - ref.float()).abs().max().item() <= 2e-2 * ref.float().abs().max().item()
+    assert calls == [long]
