@@ -145,8 +145,9 @@ class StrategoRolloutBuffer:
         return self._t["chasing_violation"].clone()
 
     def hash_board(self) -> torch.Tensor:
-        """``int64 [N]`` Zobrist hash of every board (:192-206)."""
-        out = torch.zeros(self._n, dtype=torch.int64, device=self._dev)
+        """``int64 [N]`` Zobrist hash of every board (:192-206); the kernel
+        writes every element, so the output is not cleared first."""
+        out = torch.empty(self._n, dtype=torch.int64, device=self._dev)
         self._run("atx_rollout_hash", ctypes.c_void_p(out.data_ptr()))
         return out
 
