@@ -5,13 +5,9 @@
 // 64 and num_kv_heads = num_heads.
 //
 // The sample's X rows stay in LDS while Q, K, V of one head at a time are
-// produced into LDS by MFMA and attended over; each head's output (the
-// reference's attn_out columns 64h .. 64h+63) is parked in the sample's rows
-// of y, which the workgroup alone owns.  After the last head those rows come
-// back into LDS in place of X and the output projection runs as one GEMM over
-// all heads.  Q, K, V never leave the CU; HBM sees X once and Y once (the
-// parked attention output stays in the caches), and the weights come from L2
-// (1.2 MB for E = 384, shared by every CU).
+// produced into LDS by MFMA and attended over.  Q, K, V never leave the CU;
+// HBM sees X once and Y once, and the weights come from L2 (1.2 MB for
+// E = 384, shared by every CU).
 //
 // Per head h (8 waves):
 //  A. [Q_h | K_h | V_h]^T = W_h X^T: 12 feature tiles x NP position tiles,
@@ -21,9 +17,18 @@
 //     16-bit type (where nn.Linear rounds them) and stored row-major.
 //  B. Attention, one 16-query tile per wave, as the attention kernel does
 //     it: S^T = K Q^T, row softmax in registers, O^T = V^T P^T with V^T from
-//     transposing LDS reads; O is rounded and stored to y.
-// Then Y^T = Wo O^T with wave w owning H / 2 feature tiles of Y for every
-// position, and Y (+ bias) overwrites the parked O.
+//     transposing LDS reads; O_h (the reference's attn_out columns
+//     64h .. 64h+63) is rounded.
+// The output projection Y^T = Wo O^T has wave w owning H / 2 feature tiles of
+// Y for every position, in one of two forms:
+//  * Y in registers (C3's shape): O_h goes to one of two LDS buffers, and
+//    while head h is attended over, every wave adds Wo[:, 64(h-1) ..] O_{h-1}^T
+//    (K = 64) into accumulators it keeps across the head loop;
+//  * parked (where the accumulators or the second O buffer do not fit, or
+//    where that form measured slower): O_h is stored to the sample's rows of
+//    y, which the workgroup alone owns; after the last head those rows come
+//    back into LDS in place of X and the projection runs as one GEMM (K = E).
+// Both accumulate over the same k order, so they give identical results.
 // Rounding points match the reference's bf16 modules: Q, K, V and O are
 // rounded to the 16-bit type, every product accumulates in fp32, Y is
 // rounded once at the end.
@@ -77,9 +82,26 @@ __device__ inline int eoff(int r, int c) {
 
 }  // namespace
 
+// LDS of one workgroup: X [16 np, E], Q and K [16 np, 64], V [32 ceil(np/2), 64]
+// (padding rows zero), and, when Y accumulates in registers, two O_h buffers
+// [16 np, 64].
+constexpr size_t kMhaLdsMax = 160 * 1024;
+constexpr size_t mha_lds_core(int E, int np) {
+    return (size_t)16 * np * E * 2 + (size_t)(2 * 16 * np + 32 * ((np + 1) / 2)) * kD * 2;
+}
+constexpr size_t mha_lds_o(int np) { return (size_t)16 * np * kD * 2; }
+// Y accumulated in registers across heads (H/2 feature tiles x np position
+// tiles per wave, at most 84 VGPRs) when the double-buffered O_h fits in LDS;
+// otherwise each head's O is parked in y and projected after the last head.
+// Measured on MI355X, the register form is slower for 4 heads at np = 4 and
+// for 8 heads at np <= 3 (the per-head Wo loads are exposed there), so those
+// park too.
+constexpr bool mha_y_in_regs(int H, int np) {
+    return (H / 2) * np * 4 <= 84 && mha_lds_core(64 * H, np) + 2 * mha_lds_o(np) <= kMhaLdsMax &&
+           !(H == 4 && np == 4) && !(H == 8 && np <= 3);
+}
 inline size_t mha_lds_bytes(int E, int np) {
-    const int lp = 16 * np, lv = 32 * ((np + 1) / 2);
-    return (size_t)lp * E * 2 + (size_t)(2 * lp + lv) * kD * 2;
+    return mha_lds_core(E, np) + (mha_y_in_regs(E / 64, np) ? 2 * mha_lds_o(np) : 0);
 }
 
 // [Q_h | K_h | V_h]^T feature tiles ft0 .. ft0 + NF - 1 (of 12: Q 0-3, K 4-7,
@@ -154,6 +176,110 @@ __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* 
     }
 }
 
+// Y^T += Wo[:, 64h .. 64h+63] O_h^T over the wave's FT feature tiles and every
+// position tile (K = 64: two k-steps); `wo` holds the Wo operands of head h.
+template <typename T, int FT, int NP>
+__device__ __forceinline__ void out_proj_head(f32x4 (&yacc)[FT][NP], const u32x4 (&wo)[2][FT], const lds_t* so, int m,
+                                              int g) {
+    using M = Mfma16<T>;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const u32x4 ob = lds_ld16(so + xoff<kD>(p * 16 + m, 4 * j + g));
+#pragma unroll
+            for (int f = 0; f < FT; ++f) yacc[f][p] = M::mma(wo[j][f], ob, yacc[f][p]);
+        }
+}
+
+// Attention of one head for query tile qt (rows 16 qt .. 16 qt + 15): S^T =
+// K Q^T, row softmax in registers, O^T = V^T P^T with V^T from transposing LDS
+// reads.  Returns the lane's O elements 16g .. 16g + 15 of row 16 qt + m,
+// rounded to T (where the reference's attention output is rounded), as two
+// 16-byte chunks.
+template <typename T, int NP, bool CAUSAL>
+__device__ __forceinline__ void attend_tile(const lds_t* sq, const lds_t* sk, const lds_t* sv, const int (&troff)[4],
+                                            int qt, int L, float c2, int m, int g, u32x4 (&out)[2]) {
+    using M = Mfma16<T>;
+    constexpr int NKC = (NP + 1) / 2;  // 32-key chunks
+    const float kNegInf = -__builtin_inff();
+    const int qrow = qt * 16 + m;
+    u32x4 qop[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) qop[i] = lds_ld16(sq + xoff<kD>(qrow, 4 * i + g));
+    const int kend = CAUSAL ? min(L, qt * 16 + 16) : L;  // keys >= kend are unusable for the whole tile
+    f32x4 s[NP];
+    float mx = kNegInf;
+#pragma unroll
+    for (int kt = 0; kt < NP; ++kt) {
+        if (kt * 16 < kend) {
+            f32x4 acc = M::mma(lds_ld16(sk + xoff<kD>(kt * 16 + m, g)), qop[0], f32x4{0.f, 0.f, 0.f, 0.f});
+            acc = M::mma(lds_ld16(sk + xoff<kD>(kt * 16 + m, 4 + g)), qop[1], acc);
+            if (kt * 16 + 16 > (CAUSAL ? min(L, qt * 16 + 1) : L)) {
+                u32x4 ab = __builtin_bit_cast(u32x4, acc);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = kt * 16 + 4 * g + i;
+                    const bool ok = key < L && (!CAUSAL || key <= qrow);
+                    ab[i] = ok ? ab[i] : 0xff800000u;
+                }
+                acc = __builtin_bit_cast(f32x4, ab);
+            }
+            mx = fmaxf(fmaxf(mx, acc[0]), acc[1]);
+            mx = fmaxf(fmaxf(mx, acc[2]), acc[3]);
+            s[kt] = acc;
+        }
+    }
+    mx = colgroup_max(mx);
+    const float nb = -mx * c2;  // every query sees key 0: mx is finite
+    float sum = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < NP; ++kt) {
+        if (kt * 16 < kend) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s[kt][i] = fast_exp2(__builtin_fmaf(s[kt][i], c2, nb));
+                sum += s[kt][i];
+            }
+        }
+    }
+    sum = colgroup_sum(sum);
+    const float rs = 1.f / sum;
+    // P^T packed per 32-key chunk (unnormalised; 1/sum applied to O)
+    u32x4 pk[NKC];
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) {
+        float pv[8];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int kt = 2 * c + hh;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pv[4 * hh + i] = (kt < NP && kt * 16 < kend) ? s[kt < NP ? kt : 0][i] : 0.f;
+        }
+        pk[c] = u32x4{M::pack2(pv[0], pv[1]), M::pack2(pv[2], pv[3]), M::pack2(pv[4], pv[5]), M::pack2(pv[6], pv[7])};
+    }
+    // O^T = V^T P^T: lane m (query) gets d = 16g + 4dt + i
+    f32x4 o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NKC; ++c) {
+            if (c * 32 < kend) {
+                const u32x2 lo = lds_ld8_tr16(sv + 32 * c * kD * 2 + troff[dt]);
+                const u32x2 hi = lds_ld8_tr16(sv + (32 * c + 16) * kD * 2 + troff[dt]);
+                acc = M::mma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[c], acc);
+            }
+        }
+        o[dt] = acc;
+    }
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+        out[half] = u32x4{M::pack2(o[2 * half][0] * rs, o[2 * half][1] * rs), M::pack2(o[2 * half][2] * rs, o[2 * half][3] * rs),
+                          M::pack2(o[2 * half + 1][0] * rs, o[2 * half + 1][1] * rs),
+                          M::pack2(o[2 * half + 1][2] * rs, o[2 * half + 1][3] * rs)};
+}
+
 // H heads (even), NP 16-row position tiles (L <= 16 NP).
 template <typename T, int H, int NP, bool CAUSAL>
 __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
@@ -163,17 +289,18 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
     constexpr int NKC = (NP + 1) / 2;  // 32-key chunks
     constexpr int LV = NKC * 32;       // V rows staged
     constexpr int KS = E / 32;         // k-steps of a projection
-    constexpr int FT = H / 2;                      // output feature tiles of a wave (8 groups)
-    constexpr int NPGO = kWaves / 8;               // position groups in the output projection
-    constexpr int PO = (NP + NPGO - 1) / NPGO;     // position tiles of a wave there
+    constexpr int FT = H / 2;          // output feature tiles of a wave
     constexpr int PF = KS < PFD ? KS : PFD;  // weight prefetch depth (k-steps)
     constexpr int XC = E / 8;          // 16-byte chunks per X row
+    constexpr bool YREG = mha_y_in_regs(H, NP);
     static_assert(H % 2 == 0 && H <= 8, "H even, at most 8");
+    static_assert(kWaves == 8, "wave roles assume 8 waves");
 
     lds_t* const sx0 = lds_base();
     lds_t* const sq0 = sx0 + LP * E * 2;  // Q_h
     lds_t* const sk0 = sq0 + LP * kD * 2;
     lds_t* const sv0 = sk0 + LP * kD * 2;
+    lds_t* const so0 = sv0 + LV * kD * 2;  // O_h, buffer h & 1 (Y in registers only)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -181,7 +308,6 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
     const int m = lane & 15, g = lane >> 4;
     const int b = blockIdx.x;
     const int L = a.L;
-    const float kNegInf = -__builtin_inff();
 
     // ---- X rows (rows past L read 0), V padding rows zeroed --------------------
     {
@@ -211,7 +337,6 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) rw[i] = make_rsrc(a.w[i], (uint32_t)(E * E * 2));
 
-    // Phase A roles.
     // Transposing-read offsets into V (rows 4g + t, elements a4*16 + 4dt).
     int troff[4];
 #pragma unroll
@@ -223,6 +348,17 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
     int xlane[4];
 #pragma unroll
     for (int par = 0; par < 4; ++par) xlane[par] = m * E * 2 + (((4 * par + g) ^ m) & 15) * 16;
+
+    // Output projection: wave w owns Y feature tiles FT w .. FT w + FT - 1 for
+    // every position.
+    uint32_t orow[FT];
+#pragma unroll
+    for (int f = 0; f < FT; ++f) orow[f] = (uint32_t)(((wave * FT + f) * 16 + m) * E + 8 * g) * 2;
+    f32x4 yacc[FT][NP];
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) yacc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     __syncthreads();
 
@@ -245,158 +381,100 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
         __syncthreads();
 
         // ---- B: attention of head h, one query tile per wave -------------------
-        if (wave < NP) {
-            const int qt = wave;
-            const int qrow = qt * 16 + m;
-            u32x4 qop[2];
+        if constexpr (YREG) {
+            // O_h into LDS buffer h & 1; meanwhile the output projection of head
+            // h - 1 reads buffer (h - 1) & 1, complete since the barrier above
+            // and not written again before the barrier after the next
+            // projections.
+            lds_t* const so = lds_opaque(so0);
+            u32x4 wo[2][FT];  // Wo operands of head h - 1, in flight during the attention
+            if (h > 0)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) qop[i] = lds_ld16(sq + xoff<kD>(qrow, 4 * i + g));
-            const int kend = CAUSAL ? min(L, qt * 16 + 16) : L;  // keys >= kend are unusable for the whole tile
-            f32x4 s[NP];
-            float mx = kNegInf;
+                for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int kt = 0; kt < NP; ++kt) {
-                if (kt * 16 < kend) {
-                    f32x4 acc = M::mma(lds_ld16(sk + xoff<kD>(kt * 16 + m, g)), qop[0], f32x4{0.f, 0.f, 0.f, 0.f});
-                    acc = M::mma(lds_ld16(sk + xoff<kD>(kt * 16 + m, 4 + g)), qop[1], acc);
-                    if (kt * 16 + 16 > (CAUSAL ? min(L, qt * 16 + 1) : L)) {
-                        u32x4 ab = __builtin_bit_cast(u32x4, acc);
+                    for (int f = 0; f < FT; ++f)
+                        wo[j][f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)((2 * h - 2 + j) * 32) * 2);
+            if (wave < NP) {
+                u32x4 out[2];
+                attend_tile<T, NP, CAUSAL>(sq, sk, sv, troff, wave, L, a.c2, m, g, out);
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const int key = kt * 16 + 4 * g + i;
-                            const bool ok = key < L && (!CAUSAL || key <= qrow);
-                            ab[i] = ok ? ab[i] : 0xff800000u;
-                        }
-                        acc = __builtin_bit_cast(f32x4, ab);
-                    }
-                    mx = fmaxf(fmaxf(mx, acc[0]), acc[1]);
-                    mx = fmaxf(fmaxf(mx, acc[2]), acc[3]);
-                    s[kt] = acc;
-                }
+                for (int half = 0; half < 2; ++half)
+                    lds_st16(so + (h & 1) * LP * kD * 2 + xoff<kD>(wave * 16 + m, 2 * g + half), out[half]);
             }
-            mx = colgroup_max(mx);
-            const float nb = -mx * a.c2;  // every query sees key 0: mx is finite
-            float sum = 0.f;
+            if (h > 0) out_proj_head<T, FT, NP>(yacc, wo, so + ((h - 1) & 1) * LP * kD * 2, m, g);
+        } else {
+            // O_h parked in the sample's own rows of y (the reference's
+            // attn_out columns 64h .. 64h + 63; rows past L are dropped).
+            if (wave < NP) {
+                u32x4 out[2];
+                attend_tile<T, NP, CAUSAL>(sq, sk, sv, troff, wave, L, a.c2, m, g, out);
 #pragma unroll
-            for (int kt = 0; kt < NP; ++kt) {
-                if (kt * 16 < kend) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        s[kt][i] = fast_exp2(__builtin_fmaf(s[kt][i], a.c2, nb));
-                        sum += s[kt][i];
-                    }
-                }
+                for (int half = 0; half < 2; ++half)
+                    buf_st16_cached(ry, (uint32_t)((wave * 16 + m) * a.yss + h * kD + 16 * g + 8 * half) * 2, out[half]);
             }
-            sum = colgroup_sum(sum);
-            const float rs = 1.f / sum;
-            // P^T packed per 32-key chunk (unnormalised; 1/sum applied to O)
-            u32x4 pk[NKC];
-#pragma unroll
-            for (int c = 0; c < NKC; ++c) {
-                float pv[8];
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int kt = 2 * c + hh;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) pv[4 * hh + i] = (kt < NP && kt * 16 < kend) ? s[kt < NP ? kt : 0][i] : 0.f;
-                }
-                pk[c] = u32x4{M::pack2(pv[0], pv[1]), M::pack2(pv[2], pv[3]), M::pack2(pv[4], pv[5]), M::pack2(pv[6], pv[7])};
-            }
-            // O^T = V^T P^T: lane m (query) gets d = 16g + 4dt + i
-            f32x4 o[4];
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt) {
-                f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int c = 0; c < NKC; ++c) {
-                    if (c * 32 < kend) {
-                        const u32x2 lo = lds_ld8_tr16(sv + 32 * c * kD * 2 + troff[dt]);
-                        const u32x2 hi = lds_ld8_tr16(sv + (32 * c + 16) * kD * 2 + troff[dt]);
-                        acc = M::mma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[c], acc);
-                    }
-                }
-                o[dt] = acc;
-            }
-            // O rows (rounded) go to y, which holds the sample's attention output
-            // [L, E] until the output projection overwrites it: elements
-            // 64h + 16g .. +15 of row qrow (rows past L are dropped)
-#pragma unroll
-            for (int half = 0; half < 2; ++half)
-                buf_st16_cached(ry, (uint32_t)(qrow * a.yss + h * kD + 16 * g + 8 * half) * 2,
-                                u32x4{M::pack2(o[2 * half][0] * rs, o[2 * half][1] * rs),
-                                      M::pack2(o[2 * half][2] * rs, o[2 * half][3] * rs),
-                                      M::pack2(o[2 * half + 1][0] * rs, o[2 * half + 1][1] * rs),
-                                      M::pack2(o[2 * half + 1][2] * rs, o[2 * half + 1][3] * rs)});
         }
     }
-    // Every head's O store has completed (s_waitcnt 0: acknowledged by the
-    // L2 this CU writes through) before any wave of the workgroup reads the
-    // rows back with L1-bypassing loads.  Only this workgroup touches these
-    // rows, so no wider fence (which would write back and invalidate L2) is
-    // needed.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
 
-    // ---- O (all heads) back into LDS in place of X: reads bypass L1 ------------------
-    {
-        constexpr int N = LP * XC;
-        constexpr int U = (N + kThreads - 1) / kThreads;
-        u32x4 v[U];
+    if constexpr (YREG) {
+        __syncthreads();  // every O_{H-1} row is in LDS
+        u32x4 wo[2][FT];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int idx = u * kThreads + tid;
-            const int r = idx / XC, c = idx - (idx / XC) * XC;
-            v[u] = __builtin_amdgcn_raw_buffer_load_b128(ry, (int)(idx < N ? (uint32_t)(r * a.yss + c * 8) * 2 : 0xfffffff0u),
-                                                         0, kAuxGlc);
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int f = 0; f < FT; ++f) wo[j][f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)((2 * H - 2 + j) * 32) * 2);
+        out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(so0) + ((H - 1) & 1) * LP * kD * 2, m, g);
+    } else {
+        // Every head's O store has completed (s_waitcnt 0: acknowledged by the
+        // L2 this CU writes through) before any wave of the workgroup reads the
+        // rows back with L1-bypassing loads.  Only this workgroup touches these
+        // rows, so no wider fence (which would write back and invalidate L2) is
+        // needed.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        // O (all heads) back into LDS in place of X: reads bypass L1
+        {
+            constexpr int N = LP * XC;
+            constexpr int U = (N + kThreads - 1) / kThreads;
+            u32x4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int idx = u * kThreads + tid;
+                const int r = idx / XC, c = idx - (idx / XC) * XC;
+                v[u] = __builtin_amdgcn_raw_buffer_load_b128(ry, (int)(idx < N ? (uint32_t)(r * a.yss + c * 8) * 2 : 0xfffffff0u),
+                                                             0, kAuxGlc);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int idx = u * kThreads + tid;
+                const int r = idx / XC, c = idx - (idx / XC) * XC;
+                if (idx < N) lds_st16(sx0 + eoff<E>(r, c), v[u]);
+            }
         }
+        __syncthreads();
+        // Y^T = Wo O^T as one GEMM over all heads (K = E)
+        u32x4 wbuf[PF][FT];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int idx = u * kThreads + tid;
-            const int r = idx / XC, c = idx - (idx / XC) * XC;
-            if (idx < N) lds_st16(sx0 + eoff<E>(r, c), v[u]);
-        }
-    }
-    __syncthreads();
-
-    // ---- Y^T = Wo O^T: feature tiles FT fo .. FT fo + FT-1 of position tiles
-    // po0 .. po0 + PO - 1 (fo = wave % 8; extra tiles repeat NP - 1, unstored)
-    const int fo = wave & 7, po0 = (wave >> 3) * PO;
-    f32x4 yacc[FT][PO];
+        for (int s2 = 0; s2 < PF; ++s2)
 #pragma unroll
-    for (int f = 0; f < FT; ++f)
-#pragma unroll
-        for (int p = 0; p < PO; ++p) yacc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
-    {
-        int opos[PO];
-#pragma unroll
-        for (int p = 0; p < PO; ++p) opos[p] = min(po0 + p, NP - 1) * 16 * E * 2;
-        uint32_t orow[FT];
-#pragma unroll
-        for (int f = 0; f < FT; ++f) orow[f] = (uint32_t)(((fo * FT + f) * 16 + m) * E) * 2;
-        constexpr int PFO = KS < PFD ? KS : PFD;
-        u32x4 wbuf[PFO][FT];
-#pragma unroll
-        for (int s2 = 0; s2 < PFO; ++s2)
-#pragma unroll
-            for (int f = 0; f < FT; ++f) wbuf[s2][f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)(s2 * 32 + 8 * g) * 2);
+            for (int f = 0; f < FT; ++f) wbuf[s2][f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)(s2 * 32) * 2);
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) {
             u32x4 wa[FT], nxt[FT];
 #pragma unroll
             for (int f = 0; f < FT; ++f) {
-                wa[f] = wbuf[kk % PFO][f];
-                if (kk + PFO < KS) nxt[f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)((kk + PFO) * 32 + 8 * g) * 2);
+                wa[f] = wbuf[kk % PF][f];
+                if (kk + PF < KS) nxt[f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)((kk + PF) * 32) * 2);
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int p = 0; p < PO; ++p) {
-                const u32x4 ob = lds_ld16(sx0 + xlane[kk & 3] + opos[p] + (kk >> 2) * 256);
+            for (int p = 0; p < NP; ++p) {
+                const u32x4 ob = lds_ld16(sx0 + xlane[kk & 3] + p * 16 * E * 2 + (kk >> 2) * 256);
 #pragma unroll
                 for (int f = 0; f < FT; ++f) yacc[f][p] = M::mma(wa[f], ob, yacc[f][p]);
             }
-            if (kk + PFO < KS)
+            if (kk + PF < KS)
 #pragma unroll
-                for (int f = 0; f < FT; ++f) wbuf[kk % PFO][f] = nxt[f];
+                for (int f = 0; f < FT; ++f) wbuf[kk % PF][f] = nxt[f];
         }
     }
 
@@ -404,15 +482,14 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
     const T* const bo = static_cast<const T*>(a.bias[3]);
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
-        const int feat = (fo * FT + f) * 16 + 4 * g;
+        const int feat = (wave * FT + f) * 16 + 4 * g;
         f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};
         if (bo)
 #pragma unroll
             for (int i = 0; i < 4; ++i) bv[i] = static_cast<float>(bo[feat + i]);
 #pragma unroll
-        for (int p = 0; p < PO; ++p)
-            if (po0 + p < NP)
-                buf_st8_cached(ry, (uint32_t)(((po0 + p) * 16 + m) * a.yss + feat) * 2,
+        for (int p = 0; p < NP; ++p)
+            buf_st8_cached(ry, (uint32_t)((p * 16 + m) * a.yss + feat) * 2,
                            u32x2{M::pack2(yacc[f][p][0] + bv[0], yacc[f][p][1] + bv[1]),
                                  M::pack2(yacc[f][p][2] + bv[2], yacc[f][p][3] + bv[3])});
     }
