@@ -112,7 +112,7 @@ inline size_t mha_lds_bytes(int E, int np) {
 template <typename T, int E, int NP, int NF>
 __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* sk, lds_t* sv, const int (&xlane)[4],
                                              rsrc_t rq, rsrc_t rk, rsrc_t rv, const void* const (&bias)[4], int h,
-                                             int ft0, int m, int g) {
+                                             int H, int ft0, int m, int g, u32x4 (&wpre)[NF]) {
     using M = Mfma16<T>;
     constexpr int KS = E / 32;
     f32x4 acc[NF][NP];
@@ -131,12 +131,20 @@ __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* 
     // Weight k-steps stay PF ahead of the MFMAs: each iteration issues step
     // kk + PF first, and a scheduling barrier keeps the compiler from
     // sinking those loads to their use.
+    // From 6 position tiles on, step 0 comes from `wpre`, loaded by the
+    // previous head's call (so its L2 latency passes under that head's
+    // attention), or here for head 0.  (At shorter lengths this measured
+    // slower on MI355X: each head loads step 0 at its start.)
+    constexpr bool WPRE = NP >= 6;
     constexpr int PF = KS < PFD ? KS : PFD;
     u32x4 wbuf[PF][NF];
+    if (!WPRE || h == 0)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) wpre[f] = buf_ld16_keep(wr[f], wrow[f]);
 #pragma unroll
     for (int s = 0; s < PF; ++s)
 #pragma unroll
-        for (int f = 0; f < NF; ++f) wbuf[s][f] = buf_ld16_keep(wr[f], wrow[f] + s * 64);
+        for (int f = 0; f < NF; ++f) wbuf[s][f] = s == 0 ? wpre[f] : buf_ld16_keep(wr[f], wrow[f] + s * 64);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
         u32x4 cur[NF], nxt[NF];
@@ -156,6 +164,10 @@ __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* 
 #pragma unroll
             for (int f = 0; f < NF; ++f) wbuf[kk % PF][f] = nxt[f];
     }
+    // Step 0 of head h + 1 (its rows start kD rows further down).
+    if (WPRE && h + 1 < H)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) wpre[f] = buf_ld16_keep(wr[f], wrow[f] + kD * E * 2);
     __syncthreads();  // every wave is done with the previous head's Q, K, V
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
@@ -360,6 +372,8 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
 #pragma unroll
         for (int p = 0; p < NP; ++p) yacc[f][p] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    u32x4 wpre[2], wpre1[1];  // step-0 weights of the next head (Q/K waves, V waves)
+
     __syncthreads();
 
     for (int h = 0; h < H; ++h) {
@@ -375,9 +389,9 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
         // weight element crosses from L2 once per sample and each SIMD holds
         // one 2-tile and one 1-tile wave.
         if (wave < 4)
-            project_head<T, E, NP, 2>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, 2 * wave, m, g);
+            project_head<T, E, NP, 2>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, H, 2 * wave, m, g, wpre);
         else
-            project_head<T, E, NP, 1>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, 4 + wave, m, g);
+            project_head<T, E, NP, 1>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, H, 4 + wave, m, g, wpre1);
         __syncthreads();
 
         // ---- B: attention of head h, one query tile per wave -------------------
