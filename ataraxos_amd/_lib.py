@@ -243,6 +243,8 @@ ENTRY_POINTS = {
     "atx_kq_masked_softmax_fwd": (ctypes.c_int, [ctypes.POINTER(KqParams), _ptr]),
     "atx_kq_bwd": (ctypes.c_int, [ctypes.POINTER(KqBwdParams), _ptr]),
     "atx_mha_fwd": (ctypes.c_int, [ctypes.POINTER(MhaParams), _ptr]),
+    "atx_mha_fwd_packed": (ctypes.c_int, [ctypes.POINTER(MhaParams), _ptr]),
+    "atx_mha_pack_weight": (ctypes.c_int, [_i32, _i32, _ptr, _ptr, _ptr]),
     "atx_attn_decode_fwd": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr]),
     # include/ataraxos_rollout.h
     "atx_rollout_apply": (ctypes.c_int, [_state_ptr, _ptr, _ptr]),

@@ -41,13 +41,14 @@ from . import ops
 
 __all__ = ["MultiHeadAttention", "math_attention", "FUSED_MIN_SEQ"]
 
-# Shortest sequence at which the one-launch layer (ops.mha_forward) beats the
-# unfused path (hipBLASLt projections + the attention kernel), by head count
-# at head_dim 64, measured on MI355X at B=2048/4096 in bf16.  The fused
-# layer streams every weight from L2 once per sample whatever the length, so
-# short sequences are cheaper unfused: at 8 heads (E=512) the fused layer
-# took 967 us at L=40 against 531 us unfused, and won from L=84 on.
-FUSED_MIN_SEQ = {2: 1, 4: 64, 6: 48, 8: 84}
+# Shortest sequence at which the one-launch layer (ops.mha_forward with packed
+# weights) beats the unfused path (hipBLASLt projections + the attention
+# kernel), by head count at head_dim 64, measured on MI355X through this
+# module in inference at B=4096 (8 heads: B=2048), bf16, causal and not.  The
+# fused layer streams every weight from L2 once per sample whatever the
+# length, so the shortest sequences stay cheaper unfused: at 8 heads 158 us
+# fused against 116 us unfused at L=16, 191 against 198 at L=24.
+FUSED_MIN_SEQ = {2: 1, 4: 1, 6: 16, 8: 24}
 
 
 def math_attention(
@@ -120,6 +121,11 @@ class MultiHeadAttention(nn.Module):
         self.k_proj = nn.Linear(embed_dim, kv_dim, bias=qkv_bias)
         self.v_proj = nn.Linear(embed_dim, kv_dim, bias=qkv_bias)
         self.out_proj = nn.Linear(num_heads * self.head_dim, embed_dim, bias=qkv_bias)
+        # The fused layer reads the four weights in a packed tile order; the
+        # packed copies are kept here (not in the state_dict) with the key of
+        # the weights they were made from, and remade when a weight is
+        # replaced or changed in place (its version counter moves).
+        self._packed: tuple[tuple, tuple[torch.Tensor, ...]] | None = None
 
     @property
     def backend(self) -> str:
@@ -163,12 +169,20 @@ class MultiHeadAttention(nn.Module):
         w = self.q_proj.weight
         return x.dtype == w.dtype and ops.mha_forward_supported(self.embed_dim, self.num_heads, x.shape[1], x.dtype)
 
+    def _packed_weights(self) -> tuple[torch.Tensor, ...]:
+        """q/k/v/out_proj weights in the fused kernel's packed order, cached."""
+        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.out_proj.weight)
+        key = tuple((id(w), w.data_ptr(), w._version, w.dtype) for w in ws)
+        if self._packed is None or self._packed[0] != key:
+            self._packed = (key, tuple(ops.mha_pack_weight(w.detach()) for w in ws))
+        return self._packed[1]
+
     def _forward_fused(self, x: torch.Tensor) -> torch.Tensor:
         """Projections + attention + output projection in one kernel launch."""
         return ops.mha_forward(
-            x, self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.out_proj.weight,
+            x, *self._packed_weights(),
             num_heads=self.num_heads, b_q=self.q_proj.bias, b_k=self.k_proj.bias, b_v=self.v_proj.bias,
-            b_o=self.out_proj.bias, causal=self.causal, scale=1.0 / math.sqrt(self.head_dim),
+            b_o=self.out_proj.bias, causal=self.causal, scale=1.0 / math.sqrt(self.head_dim), packed=True,
         )
 
     def _expand_kv_heads(self, k: torch.Tensor, v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

@@ -104,17 +104,36 @@ inline size_t mha_lds_bytes(int E, int np) {
     return mha_lds_core(E, np) + (mha_y_in_regs(E / 64, np) ? 2 * mha_lds_o(np) : 0);
 }
 
-// [Q_h | K_h | V_h]^T feature tiles ft0 .. ft0 + NF - 1 (of 12: Q 0-3, K 4-7,
-// V 8-11) for every position tile: X^T rows from LDS, the weight rows from
-// memory with the next k-step in flight.  Results (+ bias) are rounded and
-// stored row-major into sq / sk / sv after a workgroup barrier (all waves
-// call this once per head).
-template <typename T, int E, int NP, int NF>
+// Weights are read either as the nn.Linear matrix [E, E] (row-major: one
+// operand load covers 16 rows x 64 bytes, half of each 128-byte line) or in
+// the packed tile order that atx_mha_pack_weight writes: for row tile rt (16
+// output features) and k-step kt (32 inputs), the 64 lanes' 16-byte operand
+// chunks lie contiguous, lane 16 g + m holding row 16 rt + m, inputs
+// 32 kt + 8 g .. + 7, so one load covers 8 whole lines.  Offsets in bytes of
+// a lane's chunk at k-step 0, and the stride of one k-step:
+template <int E, bool PK>
+__device__ inline uint32_t wtile_off(int rt, int m, int g) {
+    return PK ? (uint32_t)((rt * (E / 32) * 64 + 16 * g + m) * 16) : (uint32_t)((rt * 16 + m) * E + 8 * g) * 2;
+}
+template <bool PK>
+constexpr uint32_t kWStep = PK ? 1024 : 64;
+// (In both orders the next head's rows, 4 row tiles on, lie kD * E * 2 bytes
+// further.)
+
+// [Q_h | K_h | V_h]^T feature tiles (of 12: Q 0-3, K 4-7, V 8-11): tile fta
+// for every position tile and, when NF = 2, tile ftb for position tiles
+// PB1 .. PB1 + PN1 - 1.  X^T rows come from LDS (one read per position tile
+// serves both tiles), the weight rows from memory with the next k-step in
+// flight.  Results (+ bias) are rounded and stored row-major into sq / sk / sv
+// after a workgroup barrier (all waves call this once per head).
+template <typename T, int E, int NP, int NF, int PB1, int PN1, bool PK>
 __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* sk, lds_t* sv, const int (&xlane)[4],
                                              rsrc_t rq, rsrc_t rk, rsrc_t rv, const void* const (&bias)[4], int h,
-                                             int H, int ft0, int m, int g, u32x4 (&wpre)[NF]) {
+                                             int H, int fta, int ftb, int m, int g, u32x4 (&wpre)[NF]) {
     using M = Mfma16<T>;
     constexpr int KS = E / 32;
+    // tile f covers position tile p
+    auto covers = [](int f, int p) constexpr { return f == 0 || (p >= PB1 && p < PB1 + PN1); };
     f32x4 acc[NF][NP];
 #pragma unroll
     for (int f = 0; f < NF; ++f)
@@ -124,9 +143,9 @@ __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* 
     uint32_t wrow[NF];
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-        const int ft = ft0 + f;
+        const int ft = f == 0 ? fta : ftb;
         wr[f] = (ft >> 2) == 0 ? rq : ((ft >> 2) == 1 ? rk : rv);
-        wrow[f] = (uint32_t)((h * kD + (ft & 3) * 16 + m) * E + 8 * g) * 2;
+        wrow[f] = wtile_off<E, PK>(h * 4 + (ft & 3), m, g);
     }
     // Weight k-steps stay PF ahead of the MFMAs: each iteration issues step
     // kk + PF first, and a scheduling barrier keeps the compiler from
@@ -144,21 +163,22 @@ __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* 
 #pragma unroll
     for (int s = 0; s < PF; ++s)
 #pragma unroll
-        for (int f = 0; f < NF; ++f) wbuf[s][f] = s == 0 ? wpre[f] : buf_ld16_keep(wr[f], wrow[f] + s * 64);
+        for (int f = 0; f < NF; ++f) wbuf[s][f] = s == 0 ? wpre[f] : buf_ld16_keep(wr[f], wrow[f] + s * kWStep<PK>);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
         u32x4 cur[NF], nxt[NF];
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
             cur[f] = wbuf[kk % PF][f];
-            if (kk + PF < KS) nxt[f] = buf_ld16_keep(wr[f], wrow[f] + (kk + PF) * 64);
+            if (kk + PF < KS) nxt[f] = buf_ld16_keep(wr[f], wrow[f] + (kk + PF) * kWStep<PK>);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
             const u32x4 xb = lds_ld16(sx + xlane[kk & 3] + p * 16 * E * 2 + (kk >> 2) * 256);
 #pragma unroll
-            for (int f = 0; f < NF; ++f) acc[f][p] = M::mma(cur[f], xb, acc[f][p]);
+            for (int f = 0; f < NF; ++f)
+                if (covers(f, p)) acc[f][p] = M::mma(cur[f], xb, acc[f][p]);
         }
         if (kk + PF < KS)
 #pragma unroll
@@ -171,7 +191,7 @@ __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* 
     __syncthreads();  // every wave is done with the previous head's Q, K, V
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-        const int ft = ft0 + f;
+        const int ft = f == 0 ? fta : ftb;
         f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};  // bias of features 4g .. 4g+3 of the tile
         const T* bp = static_cast<const T*>(bias[ft >> 2]);
         if (bp) {
@@ -182,6 +202,7 @@ __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* 
         lds_t* const dst = ft < 4 ? sq : (ft < 8 ? sk : sv);
 #pragma unroll
         for (int p = 0; p < NP; ++p)
+            if (covers(f, p))
             lds_st8(dst + xquad<kD>(p * 16 + m, (ft & 3) * 16 + 4 * g),
                     u32x2{M::pack2(acc[f][p][0] + bv[0], acc[f][p][1] + bv[1]),
                           M::pack2(acc[f][p][2] + bv[2], acc[f][p][3] + bv[3])});
@@ -293,7 +314,7 @@ __device__ __forceinline__ void attend_tile(const lds_t* sq, const lds_t* sk, co
 }
 
 // H heads (even), NP 16-row position tiles (L <= 16 NP).
-template <typename T, int H, int NP, bool CAUSAL>
+template <typename T, int H, int NP, bool CAUSAL, bool PK>
 __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
     using M = Mfma16<T>;
     constexpr int E = H * kD;
@@ -365,7 +386,7 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
     // every position.
     uint32_t orow[FT];
 #pragma unroll
-    for (int f = 0; f < FT; ++f) orow[f] = (uint32_t)(((wave * FT + f) * 16 + m) * E + 8 * g) * 2;
+    for (int f = 0; f < FT; ++f) orow[f] = wtile_off<E, PK>(wave * FT + f, m, g);
     f32x4 yacc[FT][NP];
 #pragma unroll
     for (int f = 0; f < FT; ++f)
@@ -389,9 +410,9 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
         // weight element crosses from L2 once per sample and each SIMD holds
         // one 2-tile and one 1-tile wave.
         if (wave < 4)
-            project_head<T, E, NP, 2>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, H, 2 * wave, m, g, wpre);
+            project_head<T, E, NP, 2, 0, NP, PK>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, H, 2 * wave, 2 * wave + 1, m, g, wpre);
         else
-            project_head<T, E, NP, 1>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, H, 4 + wave, m, g, wpre1);
+            project_head<T, E, NP, 1, 0, 0, PK>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, H, 4 + wave, 0, m, g, wpre1);
         __syncthreads();
 
         // ---- B: attention of head h, one query tile per wave -------------------
@@ -407,7 +428,7 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
                 for (int j = 0; j < 2; ++j)
 #pragma unroll
                     for (int f = 0; f < FT; ++f)
-                        wo[j][f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)((2 * h - 2 + j) * 32) * 2);
+                        wo[j][f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)(2 * h - 2 + j) * kWStep<PK>);
             if (wave < NP) {
                 u32x4 out[2];
                 attend_tile<T, NP, CAUSAL>(sq, sk, sv, troff, wave, L, a.c2, m, g, out);
@@ -435,7 +456,7 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int f = 0; f < FT; ++f) wo[j][f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)((2 * H - 2 + j) * 32) * 2);
+            for (int f = 0; f < FT; ++f) wo[j][f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)(2 * H - 2 + j) * kWStep<PK>);
         out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(so0) + ((H - 1) & 1) * LP * kD * 2, m, g);
     } else {
         // Every head's O store has completed (s_waitcnt 0: acknowledged by the
@@ -470,14 +491,14 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
 #pragma unroll
         for (int s2 = 0; s2 < PF; ++s2)
 #pragma unroll
-            for (int f = 0; f < FT; ++f) wbuf[s2][f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)(s2 * 32) * 2);
+            for (int f = 0; f < FT; ++f) wbuf[s2][f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)s2 * kWStep<PK>);
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) {
             u32x4 wa[FT], nxt[FT];
 #pragma unroll
             for (int f = 0; f < FT; ++f) {
                 wa[f] = wbuf[kk % PF][f];
-                if (kk + PF < KS) nxt[f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)((kk + PF) * 32) * 2);
+                if (kk + PF < KS) nxt[f] = buf_ld16_keep(rw[3], orow[f] + (uint32_t)(kk + PF) * kWStep<PK>);
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -523,28 +544,28 @@ int launch_mha(K kernel, int grid, size_t lds, hipStream_t st, const MhaArgs& a)
     return ATX_OK;
 }
 
-template <typename T, int H, bool CAUSAL>
+template <typename T, int H, bool CAUSAL, bool PK>
 int dispatch_mha_np(int np, int grid, size_t lds, hipStream_t st, const MhaArgs& a) {
     switch (np) {
-        case 1: return launch_mha(mha_fused<T, H, 1, CAUSAL>, grid, lds, st, a);
-        case 2: return launch_mha(mha_fused<T, H, 2, CAUSAL>, grid, lds, st, a);
-        case 3: return launch_mha(mha_fused<T, H, 3, CAUSAL>, grid, lds, st, a);
-        case 4: return launch_mha(mha_fused<T, H, 4, CAUSAL>, grid, lds, st, a);
-        case 5: return launch_mha(mha_fused<T, H, 5, CAUSAL>, grid, lds, st, a);
-        case 6: return launch_mha(mha_fused<T, H, 6, CAUSAL>, grid, lds, st, a);
-        case 7: return launch_mha(mha_fused<T, H, 7, CAUSAL>, grid, lds, st, a);
-        case 8: return launch_mha(mha_fused<T, H, 8, CAUSAL>, grid, lds, st, a);
+        case 1: return launch_mha(mha_fused<T, H, 1, CAUSAL, PK>, grid, lds, st, a);
+        case 2: return launch_mha(mha_fused<T, H, 2, CAUSAL, PK>, grid, lds, st, a);
+        case 3: return launch_mha(mha_fused<T, H, 3, CAUSAL, PK>, grid, lds, st, a);
+        case 4: return launch_mha(mha_fused<T, H, 4, CAUSAL, PK>, grid, lds, st, a);
+        case 5: return launch_mha(mha_fused<T, H, 5, CAUSAL, PK>, grid, lds, st, a);
+        case 6: return launch_mha(mha_fused<T, H, 6, CAUSAL, PK>, grid, lds, st, a);
+        case 7: return launch_mha(mha_fused<T, H, 7, CAUSAL, PK>, grid, lds, st, a);
+        case 8: return launch_mha(mha_fused<T, H, 8, CAUSAL, PK>, grid, lds, st, a);
         default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: %d position tiles", np);
     }
 }
 
-template <typename T, bool CAUSAL>
+template <typename T, bool CAUSAL, bool PK>
 int dispatch_mha(int H, int np, int grid, size_t lds, hipStream_t st, const MhaArgs& a) {
     switch (H) {
-        case 2: return dispatch_mha_np<T, 2, CAUSAL>(np, grid, lds, st, a);
-        case 4: return dispatch_mha_np<T, 4, CAUSAL>(np, grid, lds, st, a);
-        case 6: return dispatch_mha_np<T, 6, CAUSAL>(np, grid, lds, st, a);
-        case 8: return dispatch_mha_np<T, 8, CAUSAL>(np, grid, lds, st, a);
+        case 2: return dispatch_mha_np<T, 2, CAUSAL, PK>(np, grid, lds, st, a);
+        case 4: return dispatch_mha_np<T, 4, CAUSAL, PK>(np, grid, lds, st, a);
+        case 6: return dispatch_mha_np<T, 6, CAUSAL, PK>(np, grid, lds, st, a);
+        case 8: return dispatch_mha_np<T, 8, CAUSAL, PK>(np, grid, lds, st, a);
         default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: %d heads not supported (2, 4, 6, 8)", H);
     }
 }
@@ -552,40 +573,43 @@ int dispatch_mha(int H, int np, int grid, size_t lds, hipStream_t st, const MhaA
 }  // namespace
 }  // namespace atx
 
-extern "C" int atx_mha_fwd(const AtxMhaParams* p, void* stream) {
-    using namespace atx;
+namespace atx {
+namespace {
+
+int mha_fwd(const AtxMhaParams* p, void* stream, bool packed) {
+    const char* const fn = packed ? "atx_mha_fwd_packed" : "atx_mha_fwd";
     clear_error();
-    if (!p) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: params is NULL");
+    if (!p) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: params is NULL", fn);
     if (p->abi_version != ATX_ABI_VERSION)
-        ATX_FAIL(ATX_ERR_ABI, "atx_mha_fwd: abi_version %d, library is %d", p->abi_version, ATX_ABI_VERSION);
+        ATX_FAIL(ATX_ERR_ABI, "%s: abi_version %d, library is %d", fn, p->abi_version, ATX_ABI_VERSION);
     if (p->dtype != ATX_DTYPE_BF16 && p->dtype != ATX_DTYPE_FP16) {
-        if (p->dtype == ATX_DTYPE_FP32) ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: fp32 is not supported");
-        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: unknown dtype %d", p->dtype);
+        if (p->dtype == ATX_DTYPE_FP32) ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: fp32 is not supported", fn);
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: unknown dtype %d", fn, p->dtype);
     }
     if (p->batch < 1 || p->seq < 1 || p->num_heads < 1)
-        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: sizes must be >= 1");
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: sizes must be >= 1", fn);
     if (p->embed_dim != p->num_heads * 64)
-        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: head_dim %d not supported (64)",
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: head_dim %d not supported (64)", fn,
                  p->num_heads > 0 ? p->embed_dim / p->num_heads : 0);
     if (!p->x || !p->w_q || !p->w_k || !p->w_v || !p->w_o || !p->y)
-        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: null tensor pointer");
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: null tensor pointer", fn);
     if (!(p->scale > 0.f) || p->scale == __builtin_inff())
-        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: scale must be finite and > 0 (got %g)", (double)p->scale);
-    if (p->seq > 128) ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: seq %d not supported (<= 128)", p->seq);
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: scale must be finite and > 0 (got %g)", fn, (double)p->scale);
+    if (p->seq > 128) ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: seq %d not supported (<= 128)", fn, p->seq);
     const int E = p->embed_dim, L = p->seq;
     const int64_t xss = L == 1 ? E : p->x_stride_s, yss = L == 1 ? E : p->y_stride_s;
     if (!aligned16(p->x) || !aligned16(p->y) || ((p->x_stride_b * 2) & 15) || ((xss * 2) & 15) ||
         ((p->y_stride_b * 2) & 15) || ((yss * 2) & 15))
-        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: x/y rows must start on a 16-byte boundary");
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: x/y rows must start on a 16-byte boundary", fn);
     if (!aligned16(p->w_q) || !aligned16(p->w_k) || !aligned16(p->w_v) || !aligned16(p->w_o))
-        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: weights must be 16-byte aligned, contiguous [E, E]");
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: weights must be 16-byte aligned, contiguous [E, E]", fn);
     if (xss < 0 || yss < E || (int64_t)(L + 16) * xss * 2 + E * 2 > 0x7fffffffLL ||
         (int64_t)(L + 16) * yss * 2 + E * 2 > 0x7fffffffLL)
-        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_fwd: row strides must be >= 0 (y: >= embed_dim) and one sample < 2 GiB");
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: row strides must be >= 0 (y: >= embed_dim) and one sample < 2 GiB", fn);
     const int np = (L + 15) / 16;
     const size_t lds = mha_lds_bytes(E, np);
     if (lds > 160 * 1024)
-        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: seq %d, embed_dim %d need %zu bytes of LDS (> 160 KiB)", L, E, lds);
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: seq %d, embed_dim %d need %zu bytes of LDS (> 160 KiB)", fn, L, E, lds);
 
     MhaArgs a;
     a.x = p->x; a.xsb = p->x_stride_b; a.xss = (int)xss;
@@ -596,9 +620,55 @@ extern "C" int atx_mha_fwd(const AtxMhaParams* p, void* stream) {
     a.c2 = p->scale * kLog2e;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int H = p->num_heads;
-    if (p->dtype == ATX_DTYPE_BF16)
-        return p->causal ? dispatch_mha<__bf16, true>(H, np, p->batch, lds, st, a)
-                         : dispatch_mha<__bf16, false>(H, np, p->batch, lds, st, a);
-    return p->causal ? dispatch_mha<_Float16, true>(H, np, p->batch, lds, st, a)
-                     : dispatch_mha<_Float16, false>(H, np, p->batch, lds, st, a);
+    const bool bf = p->dtype == ATX_DTYPE_BF16;
+    if (packed) {
+        if (bf) return p->causal ? dispatch_mha<__bf16, true, true>(H, np, p->batch, lds, st, a)
+                                 : dispatch_mha<__bf16, false, true>(H, np, p->batch, lds, st, a);
+        return p->causal ? dispatch_mha<_Float16, true, true>(H, np, p->batch, lds, st, a)
+                         : dispatch_mha<_Float16, false, true>(H, np, p->batch, lds, st, a);
+    }
+    if (bf) return p->causal ? dispatch_mha<__bf16, true, false>(H, np, p->batch, lds, st, a)
+                             : dispatch_mha<__bf16, false, false>(H, np, p->batch, lds, st, a);
+    return p->causal ? dispatch_mha<_Float16, true, false>(H, np, p->batch, lds, st, a)
+                     : dispatch_mha<_Float16, false, false>(H, np, p->batch, lds, st, a);
+}
+
+// Packed tile order of one [E, E] weight (see wtile_off): thread i writes
+// 16-byte chunk i of the packed matrix.
+__global__ __launch_bounds__(256) void mha_pack_weight(const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int E) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int ks = E / 32;
+    if (i >= E * ks * 4) return;  // E * E / 8 chunks
+    const int lane = i & 63, t = i >> 6;
+    const int kt = t % ks, rt = t / ks;
+    const int m = lane & 15, g = lane >> 4;
+    st16(out + (size_t)i * 8, ld16(w + (size_t)(rt * 16 + m) * E + kt * 32 + g * 8));
+}
+
+}  // namespace
+}  // namespace atx
+
+extern "C" int atx_mha_fwd(const AtxMhaParams* p, void* stream) { return atx::mha_fwd(p, stream, false); }
+
+extern "C" int atx_mha_fwd_packed(const AtxMhaParams* p, void* stream) { return atx::mha_fwd(p, stream, true); }
+
+extern "C" int atx_mha_pack_weight(int dtype, int dim, const void* w, void* packed, void* stream) {
+    using namespace atx;
+    clear_error();
+    if (dtype != ATX_DTYPE_BF16 && dtype != ATX_DTYPE_FP16)
+        ATX_FAIL(dtype == ATX_DTYPE_FP32 ? ATX_ERR_UNSUPPORTED : ATX_ERR_INVALID_ARGUMENT,
+                 "atx_mha_pack_weight: dtype %d (16-bit only)", dtype);
+    if (dim < 32 || dim % 32 || dim > 4096)
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_pack_weight: dim %d must be a multiple of 32 in [32, 4096]", dim);
+    if (!w || !packed) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_pack_weight: null tensor pointer");
+    if (!aligned16(w) || !aligned16(packed))
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_pack_weight: weights must be 16-byte aligned");
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(w), pa = reinterpret_cast<uintptr_t>(packed);
+    const uintptr_t bytes = (uintptr_t)dim * dim * 2;
+    if (wa < pa + bytes && pa < wa + bytes) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_mha_pack_weight: w and packed overlap");
+    const int chunks = dim * dim / 8;
+    hipLaunchKernelGGL(mha_pack_weight, dim3((chunks + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(w), static_cast<uint16_t*>(packed), dim);
+    ATX_CHECK_LAUNCH("atx_mha_pack_weight launch");
+    return ATX_OK;
 }

@@ -436,12 +436,17 @@ def mha_forward(
     causal: bool = False,
     scale: float | None = None,
     out: torch.Tensor | None = None,
+    packed: bool = False,
 ) -> torch.Tensor:
     """Whole self-attention layer in one launch (no autograd):
     ``out_proj(attention(q_proj(x), k_proj(x), v_proj(x)))`` with the
     ``nn.Linear`` weights ``[E, E]`` and optional biases ``[E]``.  x ``[B, L, E]``
     -> ``[B, L, E]`` in x's dtype.  Q, K, V and the attention output are
-    rounded to x's dtype, as the reference's bf16 modules round them."""
+    rounded to x's dtype, as the reference's bf16 modules round them.
+
+    ``packed=True``: the four weights are the outputs of
+    :func:`mha_pack_weight` (``atx_mha_fwd_packed``, the faster kernel;
+    identical results)."""
     _require_device("mha_forward", x, w_q, w_k, w_v, w_o)
     if x.dim() != 3:
         raise ValueError("mha_forward: x must be [batch, seq, embed_dim]")
@@ -480,7 +485,23 @@ def mha_forward(
     p.b_q, p.b_k, p.b_v, p.b_o = (t.data_ptr() if t is not None else None for t in biases)
     p.y, p.y_stride_b, p.y_stride_s = out.data_ptr(), out.stride(0), out.stride(1)
     p.scale = float(scale)
-    _lib.check(_lib.call("atx_mha_fwd", p, _stream(x)), "atx_mha_fwd")
+    name = "atx_mha_fwd_packed" if packed else "atx_mha_fwd"
+    _lib.check(_lib.call(name, p, _stream(x)), name)
+    return out
+
+
+def mha_pack_weight(w: torch.Tensor) -> torch.Tensor:
+    """An ``nn.Linear`` weight ``[E, E]`` (bf16 / fp16, on the GPU) rearranged
+    into the tile order :func:`mha_forward` reads with ``packed=True``
+    (``atx_mha_pack_weight``); a new tensor of the same shape and dtype."""
+    _require_device("mha_pack_weight", w)
+    if w.dim() != 2 or w.shape[0] != w.shape[1] or w.dtype not in _BWD_DTYPES:
+        raise ValueError("mha_pack_weight: w must be a square bf16/fp16 matrix")
+    if not w.is_contiguous() or w.data_ptr() % 16:
+        w = w.contiguous().clone()
+    out = torch.empty_like(w, memory_format=torch.contiguous_format)
+    rc = _lib.load().atx_mha_pack_weight(_DTYPES[w.dtype], w.shape[0], w.data_ptr(), out.data_ptr(), _stream(w))
+    _lib.check(rc, "atx_mha_pack_weight")
     return out
 
 

@@ -287,6 +287,27 @@ typedef struct AtxMhaParams {
  */
 int atx_mha_fwd(const AtxMhaParams* params, void* stream);
 
+/*
+ * The same layer with w_q, w_k, w_v and w_o in the packed tile order that
+ * atx_mha_pack_weight writes (everything else as atx_mha_fwd; identical
+ * results).  The kernel's weight loads then read whole cache lines: at the
+ * Move-network shape this is ~10 % faster, at 40-64 positions up to 2x.
+ * The weights are those of attention.py:113-116 (q/k/v/out_proj), packed
+ * once per weight update by the caller; the reference has no counterpart.
+ */
+int atx_mha_fwd_packed(const AtxMhaParams* params, void* stream);
+
+/*
+ * packed = w [dim, dim] (nn.Linear weight, out x in, contiguous, 16-bit
+ * dtype) in the packed tile order: for row tile rt = 0 .. dim/16 - 1 and
+ * k-step kt = 0 .. dim/32 - 1, 64 chunks of 8 elements, chunk 16 g + m
+ * holding w[16 rt + m, 32 kt + 8 g .. 32 kt + 8 g + 7], at element offset
+ * ((rt * (dim / 32) + kt) * 64 + 16 g + m) * 8.  dim a multiple of 32 up to
+ * 4096; w and packed 16-byte aligned and not overlapping.  Asynchronous on
+ * `stream`.
+ */
+int atx_mha_pack_weight(int32_t dtype, int32_t dim, const void* w, void* packed, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Single-query attention over a KV cache (incremental decode)              */
 /* ------------------------------------------------------------------------ */

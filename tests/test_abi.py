@@ -10,6 +10,7 @@
 from __future__ import annotations
 
 import ctypes
+import itertools
 import re
 import shutil
 import subprocess
@@ -250,7 +251,8 @@ def test_fused_layer_validation_codes():
     p.x_stride_s = p.y_stride_s = 384
     p.scale = 0.125
     assert _lib.load().atx_mha_fwd(None, None) == _lib.ERR_INVALID_ARGUMENT
-    for field, value, code, text in [
+    assert _lib.load().atx_mha_fwd_packed(None, None) == _lib.ERR_INVALID_ARGUMENT
+    for (field, value, code, text), name in itertools.product([
         ("abi_version", 3, _lib.ERR_ABI, "abi_version"),
         ("dtype", _lib.DTYPE_FP32, _lib.ERR_UNSUPPORTED, "fp32"),
         ("embed_dim", 400, _lib.ERR_UNSUPPORTED, "head_dim"),
@@ -260,14 +262,33 @@ def test_fused_layer_validation_codes():
         ("scale", -1.0, _lib.ERR_INVALID_ARGUMENT, "scale"),
         ("x_stride_s", 388, _lib.ERR_INVALID_ARGUMENT, "16-byte"),
         ("y_stride_s", 192, _lib.ERR_INVALID_ARGUMENT, "strides"),
-    ]:
+    ], ("atx_mha_fwd", "atx_mha_fwd_packed")):
         saved = getattr(p, field)
         setattr(p, field, value)
-        _expect("atx_mha_fwd", p, code, text)
+        _expect(name, p, code, text)
+        assert name in _lib.last_error()
         setattr(p, field, saved)
     p.embed_dim, p.num_heads, p.seq = 512, 8, 128
     p.x_stride_s = p.y_stride_s = 512
     _expect("atx_mha_fwd", p, _lib.ERR_UNSUPPORTED, "LDS")
+    _expect("atx_mha_fwd_packed", p, _lib.ERR_UNSUPPORTED, "LDS")
+
+
+def test_weight_pack_validation_codes():
+    """atx_mha_pack_weight rejects every bad argument before touching memory."""
+    lib = _lib.load()
+    a, b = 1 << 20, 1 << 24  # never dereferenced
+    for args, code, text in [
+        ((_lib.DTYPE_FP32, 384, a, b), _lib.ERR_UNSUPPORTED, "16-bit"),
+        ((9, 384, a, b), _lib.ERR_INVALID_ARGUMENT, "dtype"),
+        ((_lib.DTYPE_BF16, 48, a, b), _lib.ERR_INVALID_ARGUMENT, "multiple of 32"),
+        ((_lib.DTYPE_BF16, 8192, a, b), _lib.ERR_INVALID_ARGUMENT, "multiple of 32"),
+        ((_lib.DTYPE_BF16, 384, None, b), _lib.ERR_INVALID_ARGUMENT, "null"),
+        ((_lib.DTYPE_BF16, 384, a + 8, b), _lib.ERR_INVALID_ARGUMENT, "aligned"),
+        ((_lib.DTYPE_BF16, 384, a, a + 1024), _lib.ERR_INVALID_ARGUMENT, "overlap"),
+    ]:
+        assert lib.atx_mha_pack_weight(*args, None) == code, args
+        assert text in _lib.last_error(), (args, _lib.last_error())
 
 
 def test_decode_validation_codes():

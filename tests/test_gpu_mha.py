@@ -171,7 +171,7 @@ def test_rejects_unsupported(cuda):
         ops.mha_forward(xb, wb, wb, wb, wb, num_heads=3)  # head_dim 128
 
 
-@pytest.mark.parametrize("heads,short,long", [(6, 40, 48), (8, 40, 100), (4, 48, 64)])
+@pytest.mark.parametrize("heads,short,long", [(6, 8, 16), (8, 16, 24), (8, 8, 40)])
 def test_module_takes_the_fused_layer_only_where_it_is_faster(cuda, monkeypatch, heads, short, long):
     """Below FUSED_MIN_SEQ the module runs the unfused path (measured faster
     there); from it on, the one-launch layer."""
@@ -192,3 +192,80 @@ def test_module_takes_the_fused_layer_only_where_it_is_faster(cuda, monkeypatch,
             got = m(x)
             assert (got.float() - ref.float()).abs().max().item() <= 2e-2 * ref.float().abs().max().item()
     assert calls == [long]
+
+
+# ---- packed weights (atx_mha_pack_weight + atx_mha_fwd_packed) ---------------
+
+
+@pytest.mark.parametrize("e,dtype", [(128, torch.bfloat16), (384, torch.bfloat16), (512, torch.float16), (96, torch.bfloat16)])
+def test_pack_weight_layout(cuda, e, dtype):
+    """The packed order is the header's formula: element
+    ((rt * (e / 32) + kt) * 64 + 16 g + m) * 8 + i holds w[16 rt + m, 32 kt + 8 g + i],
+    restated as a view/permute of w (row tile, row, k-step, group, element)."""
+    _announce(f"pack weight e={e} {dtype}")
+    w = randn((e, e), 300 + e, dtype)
+    ref = w.view(e // 16, 16, e // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(e, e)
+    got = ops.mha_pack_weight(w.to(cuda)).cpu()
+    assert torch.equal(got, ref)
+    # spot checks of the formula itself, element by element
+    flat = got.reshape(-1)
+    for rt, kt, g_, m, i in [(0, 0, 0, 0, 0), (1, 2, 3, 5, 7), (e // 16 - 1, e // 32 - 1, 3, 15, 7)]:
+        assert flat[((rt * (e // 32) + kt) * 64 + 16 * g_ + m) * 8 + i] == w[16 * rt + m, 32 * kt + 8 * g_ + i]
+
+
+@pytest.mark.parametrize(
+    "b,l,h,dtype,causal,bias",
+    [
+        (8, 100, 6, torch.bfloat16, False, False),
+        (4, 100, 8, torch.bfloat16, False, False),
+        (4, 40, 8, torch.bfloat16, True, False),
+        (4, 64, 4, torch.float16, False, True),
+        (3, 128, 2, torch.bfloat16, True, True),
+        (3, 17, 6, torch.bfloat16, False, False),
+        (5, 1, 4, torch.bfloat16, False, False),
+        (3, 112, 8, torch.float16, True, True),
+    ],
+)
+def test_packed_equals_row_major(cuda, b, l, h, dtype, causal, bias):
+    """atx_mha_fwd_packed reads the same weights in another order and does the
+    same arithmetic: bit-identical to atx_mha_fwd, which the float64 oracle
+    pins (the tests above)."""
+    e = 64 * h
+    _announce(f"mha packed b={b} l={l} h={h} {dtype} causal={causal} bias={bias}")
+    x = randn((b, l, e), 400 + l + h, dtype).to(cuda)
+    ws, bs = layer(e, dtype, 401 + l + h, bias)
+    wd = [w.to(cuda) for w in ws]
+    bd = [t.to(cuda) if t is not None else None for t in bs]
+    kw = dict(num_heads=h, b_q=bd[0], b_k=bd[1], b_v=bd[2], b_o=bd[3], causal=causal)
+    plain = ops.mha_forward(x, *wd, **kw)
+    packed = ops.mha_forward(x, *[ops.mha_pack_weight(w) for w in wd], packed=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.isfinite(plain.float()).all()
+    assert torch.equal(plain, packed)
+
+
+def test_module_repacks_after_a_weight_update(cuda):
+    """The module's cached packed weights follow in-place updates (an
+    optimizer step, load_state_dict) and replaced parameters."""
+    _announce("mha module packed-weight cache")
+    torch.manual_seed(9)
+    m = MultiHeadAttention(384, 6).to(cuda, torch.bfloat16).eval()
+    x = randn((4, 100, 384), 72, torch.bfloat16).to(cuda)
+
+    def direct():
+        return ops.mha_forward(x, m.q_proj.weight, m.k_proj.weight, m.v_proj.weight, m.out_proj.weight, num_heads=6)
+
+    with torch.no_grad():
+        y0 = m(x)
+        assert torch.equal(y0, direct())
+        m.k_proj.weight.mul_(1.5)  # in place: version counter moves
+        y1 = m(x)
+        assert not torch.equal(y1, y0)
+        assert torch.equal(y1, direct())
+        m.load_state_dict({k: v * 0.5 for k, v in m.state_dict().items()})
+        y2 = m(x)
+        assert torch.equal(y2, direct())
+        m.v_proj.weight = torch.nn.Parameter(torch.flip(m.v_proj.weight, dims=[0]))  # replaced
+        y3 = m(x)
+        assert torch.equal(y3, direct())
+        assert not torch.equal(y3, y2)
