@@ -170,8 +170,13 @@ class MultiHeadAttention(nn.Module):
         return x.dtype == w.dtype and ops.mha_forward_supported(self.embed_dim, self.num_heads, x.shape[1], x.dtype)
 
     def _packed_weights(self) -> tuple[torch.Tensor, ...]:
-        """q/k/v/out_proj weights in the fused kernel's packed order, cached."""
+        """q/k/v/out_proj weights in the fused kernel's packed order, cached.
+        Weights created under ``torch.inference_mode()`` carry no version
+        counter (their in-place changes are not tracked), so those are packed
+        on every call instead."""
         ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.out_proj.weight)
+        if any(w.is_inference() for w in ws):
+            return tuple(ops.mha_pack_weight(w.detach()) for w in ws)
         key = tuple((id(w), w.data_ptr(), w._version, w.dtype) for w in ws)
         if self._packed is None or self._packed[0] != key:
             self._packed = (key, tuple(ops.mha_pack_weight(w.detach()) for w in ws))

@@ -269,3 +269,20 @@ def test_module_repacks_after_a_weight_update(cuda):
         y3 = m(x)
         assert torch.equal(y3, direct())
         assert not torch.equal(y3, y2)
+
+
+def test_module_built_under_inference_mode(cuda):
+    """Parameters created under inference_mode have no version counter: the
+    module packs them on every call, so in-place changes still take effect."""
+    _announce("mha module under inference_mode")
+    x = randn((4, 100, 384), 73, torch.bfloat16).to(cuda)
+    with torch.inference_mode():
+        torch.manual_seed(10)
+        m = MultiHeadAttention(384, 6).to(cuda, torch.bfloat16).eval()
+        assert m.q_proj.weight.is_inference()
+        y0 = m(x)
+        m.q_proj.weight.mul_(-1.0)
+        y1 = m(x)
+        direct = ops.mha_forward(x, m.q_proj.weight, m.k_proj.weight, m.v_proj.weight, m.out_proj.weight, num_heads=6)
+    assert not torch.equal(y0, y1)
+    assert torch.equal(y1, direct)
