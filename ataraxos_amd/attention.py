@@ -39,7 +39,7 @@ import torch.nn.functional as F  # noqa: N812
 
 from . import ops
 
-__all__ = ["MultiHeadAttention", "math_attention", "FUSED_MIN_SEQ"]
+__all__ = ["MultiHeadAttention", "math_attention", "packed_weights", "FUSED_MIN_SEQ"]
 
 # Shortest sequence at which the one-launch layer (ops.mha_forward with packed
 # weights) beats the unfused path (hipBLASLt projections + the attention
@@ -49,6 +49,26 @@ __all__ = ["MultiHeadAttention", "math_attention", "FUSED_MIN_SEQ"]
 # length, so the shortest sequences stay cheaper unfused: at 8 heads 158 us
 # fused against 116 us unfused at L=16, 191 against 198 at L=24.
 FUSED_MIN_SEQ = {2: 1, 4: 1, 6: 16, 8: 24}
+
+
+def packed_weights(
+    owner: nn.Module, sources: tuple[torch.Tensor, ...], ws: tuple[torch.Tensor, ...]
+) -> tuple[torch.Tensor, ...]:
+    """The ``[E, E]`` weights ``ws`` (views of the parameters ``sources``) in
+    the fused kernel's packed order (:func:`ops.mha_pack_weight`), cached on
+    ``owner`` (a plain attribute, not in the state_dict) under the identity,
+    address and version counter of ``sources``: replacing a parameter or
+    changing it in place (an optimizer step, ``load_state_dict``) makes the
+    next call repack.  Parameters created under ``torch.inference_mode()``
+    carry no version counter, so those are packed on every call."""
+    if any(t.is_inference() for t in sources):
+        return tuple(ops.mha_pack_weight(w.detach()) for w in ws)
+    key = tuple((id(t), t.data_ptr(), t._version, t.dtype) for t in sources)
+    cache = getattr(owner, "_packed", None)
+    if cache is None or cache[0] != key:
+        cache = (key, tuple(ops.mha_pack_weight(w.detach()) for w in ws))
+        owner._packed = cache
+    return cache[1]
 
 
 def math_attention(
@@ -170,17 +190,9 @@ class MultiHeadAttention(nn.Module):
         return x.dtype == w.dtype and ops.mha_forward_supported(self.embed_dim, self.num_heads, x.shape[1], x.dtype)
 
     def _packed_weights(self) -> tuple[torch.Tensor, ...]:
-        """q/k/v/out_proj weights in the fused kernel's packed order, cached.
-        Weights created under ``torch.inference_mode()`` carry no version
-        counter (their in-place changes are not tracked), so those are packed
-        on every call instead."""
+        """q/k/v/out_proj weights in the fused kernel's packed order, cached."""
         ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.out_proj.weight)
-        if any(w.is_inference() for w in ws):
-            return tuple(ops.mha_pack_weight(w.detach()) for w in ws)
-        key = tuple((id(w), w.data_ptr(), w._version, w.dtype) for w in ws)
-        if self._packed is None or self._packed[0] != key:
-            self._packed = (key, tuple(ops.mha_pack_weight(w.detach()) for w in ws))
-        return self._packed[1]
+        return packed_weights(self, ws, ws)
 
     def _forward_fused(self, x: torch.Tensor) -> torch.Tensor:
         """Projections + attention + output projection in one kernel launch."""

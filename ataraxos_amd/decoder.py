@@ -24,6 +24,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
+from .attention import FUSED_MIN_SEQ, packed_weights
 
 __all__ = ["KernelMultiheadAttention", "use_hip_attention"]
 
@@ -38,7 +39,16 @@ class KernelMultiheadAttention(nn.MultiheadAttention):
     raises on the GPU instead of silently taking another path.  On the CPU,
     and in training with dropout > 0 (the kernel has no dropout), the forward
     is ``nn.MultiheadAttention``'s own, as in the reference.
+
+    Self-attention (``query``, ``key`` and ``value`` the same tensor, as
+    ``TransformerDecoderLayer`` calls it) without a key padding mask and
+    without autograd runs as one launch of the fused layer
+    (``ops.mha_forward``, packed weights cached on the module) where that is
+    faster (``FUSED_MIN_SEQ``, head_dim 64); ``fuse_layer = False`` keeps the
+    projections + attention kernel path.
     """
+
+    fuse_layer: bool = True  # class default: converted modules skip __init__
 
     def forward(  # type: ignore[override]
         self,
@@ -64,6 +74,7 @@ class KernelMultiheadAttention(nn.MultiheadAttention):
             )
         if key_padding_mask is not None and key_padding_mask.dtype != torch.bool:
             raise NotImplementedError("KernelMultiheadAttention on the GPU takes a bool key_padding_mask")
+        self_attention = query is key and key is value
         if not self.batch_first:
             query, key, value = (t.transpose(0, 1) for t in (query, key, value))
         b, sq, e = query.shape
@@ -77,6 +88,15 @@ class KernelMultiheadAttention(nn.MultiheadAttention):
         b_q = b_k = b_v = None
         if self.in_proj_bias is not None:
             b_q, b_k, b_v = self.in_proj_bias.chunk(3)
+        if self_attention and key_padding_mask is None and self._fused_ok(query):
+            assert self.in_proj_weight is not None
+            ws = (w_q, w_k, w_v, self.out_proj.weight)
+            out = ops.mha_forward(
+                query, *packed_weights(self, (self.in_proj_weight, self.out_proj.weight), ws),
+                num_heads=h, b_q=b_q, b_k=b_k, b_v=b_v, b_o=self.out_proj.bias, causal=is_causal,
+                scale=d**-0.5, packed=True,
+            )
+            return (out if self.batch_first else out.transpose(0, 1)), None
         q = F.linear(query, w_q, b_q).view(b, sq, h, d)
         k = F.linear(key, w_k, b_k).view(b, skv, h, d)
         v = F.linear(value, w_v, b_v).view(b, skv, h, d)
@@ -85,6 +105,21 @@ class KernelMultiheadAttention(nn.MultiheadAttention):
         if not self.batch_first:
             out = out.transpose(0, 1)
         return out, None
+
+
+    def _fused_ok(self, x: torch.Tensor) -> bool:
+        """The one-launch layer applies to self-attention over ``x``
+        ``[B, S, E]``: no autograd, packed q/k/v weights, head_dim 64, a
+        16-bit dtype matching the weights, and a sequence at least
+        ``FUSED_MIN_SEQ`` long for the head count."""
+        if not self.fuse_layer or not self._qkv_same_embed_dim or self.in_proj_weight is None:
+            return False
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            return False
+        e, h, s = self.embed_dim, self.num_heads, x.shape[1]
+        if e != 64 * h or x.dtype != self.in_proj_weight.dtype or s < FUSED_MIN_SEQ.get(h, 1 << 30):
+            return False
+        return ops.mha_forward_supported(e, h, s, x.dtype)
 
 
 def use_hip_attention(module: nn.Module) -> nn.Module:

@@ -76,3 +76,37 @@ def test_setup_decoder_matches_prefix_recompute(cuda, dtype, tol):
         if t == 0:
             assert _rel(v.cpu(), v_ref) <= tol and _rel(e.cpu(), e_ref) <= tol
     assert worst <= tol
+
+
+def test_decoder_self_attention_takes_the_fused_layer(cuda, monkeypatch):
+    """In inference, TransformerDecoderLayer's self-attention (self_attn(x, x, x),
+    causal hint, 8 heads x 64, 40 tokens) runs as one launch of the fused
+    layer with the packed in_proj slices; it equals the projections +
+    attention kernel path to bf16 rounding and the row-major fused call
+    bit for bit.  With a key padding mask it keeps the unfused path."""
+    from ataraxos_amd import ops
+    import ataraxos_amd.decoder as dec_mod
+
+    _announce("decoder self-attention fused")
+    torch.manual_seed(3)
+    m = use_hip_attention(torch.nn.MultiheadAttention(512, 8, batch_first=True)).to(cuda, torch.bfloat16).eval()
+    x = torch.randn(6, 40, 512, device=cuda).bfloat16()
+    calls = []
+    real = ops.mha_forward
+    monkeypatch.setattr(dec_mod.ops, "mha_forward", lambda *a, **k: calls.append(k.get("packed")) or real(*a, **k))
+    with torch.no_grad():
+        fused, _ = m(x, x, x, need_weights=False, is_causal=True, attn_mask=torch.zeros(40, 40, device=cuda))
+        assert calls == [True]
+        w_q, w_k, w_v = m.in_proj_weight.chunk(3)
+        b_q, b_k, b_v = m.in_proj_bias.chunk(3)
+        direct = real(x, w_q, w_k, w_v, m.out_proj.weight, num_heads=8, b_q=b_q, b_k=b_k, b_v=b_v,
+                      b_o=m.out_proj.bias, causal=True)
+        m.fuse_layer = False
+        unfused, _ = m(x, x, x, need_weights=False, is_causal=True, attn_mask=torch.zeros(40, 40, device=cuda))
+        m.fuse_layer = True
+        pad = torch.zeros(6, 40, dtype=torch.bool, device=cuda)
+        padded, _ = m(x, x, x, need_weights=False, key_padding_mask=pad)
+    assert calls == [True]  # neither fuse_layer=False nor the padded call went fused
+    assert torch.equal(fused, direct)
+    assert _rel(fused, unfused) <= 2e-2
+    assert torch.isfinite(padded.float()).all()
