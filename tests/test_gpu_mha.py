@@ -37,9 +37,9 @@ def layer(e, dtype, seed, bias=False):
     return ws, bs
 
 
-def run_case(cuda, b, l, h, dtype=torch.bfloat16, causal=False, bias=False, seed=0, x_view=False):
+def run_case(cuda, b, l, h, dtype=torch.bfloat16, causal=False, bias=False, seed=0, x_view=False, packed=False):
     e = 64 * h
-    _announce(f"mha b={b} l={l} h={h} {dtype} causal={causal} bias={bias} view={x_view}")
+    _announce(f"mha b={b} l={l} h={h} {dtype} causal={causal} bias={bias} view={x_view} packed={packed}")
     x = randn((b, l, e), seed, dtype)
     ws, bs = layer(e, dtype, seed + 1, bias)
     if x_view:  # rows of a wider buffer, NaN after the sequence and in the padding columns
@@ -49,8 +49,10 @@ def run_case(cuda, b, l, h, dtype=torch.bfloat16, causal=False, bias=False, seed
     else:
         xd = x.to(cuda)
     wd = [w.to(cuda) for w in ws]
+    if packed:
+        wd = [ops.mha_pack_weight(w) for w in wd]
     bd = [t.to(cuda) if t is not None else None for t in bs]
-    y = ops.mha_forward(xd, *wd, num_heads=h, b_q=bd[0], b_k=bd[1], b_v=bd[2], b_o=bd[3], causal=causal)
+    y = ops.mha_forward(xd, *wd, num_heads=h, b_q=bd[0], b_k=bd[1], b_v=bd[2], b_o=bd[3], causal=causal, packed=packed)
     torch.cuda.synchronize()
     names = ("q_proj", "k_proj", "v_proj", "out_proj")
     weights = {f"{n}.weight": to_np64(w) for n, w in zip(names, ws)}
@@ -211,6 +213,27 @@ def test_pack_weight_layout(cuda, e, dtype):
     flat = got.reshape(-1)
     for rt, kt, g_, m, i in [(0, 0, 0, 0, 0), (1, 2, 3, 5, 7), (e // 16 - 1, e // 32 - 1, 3, 15, 7)]:
         assert flat[((rt * (e // 32) + kt) * 64 + 16 * g_ + m) * 8 + i] == w[16 * rt + m, 32 * kt + 8 * g_ + i]
+
+
+def _random_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        h = int(rng.choice([2, 4, 6, 8]))
+        l = int(rng.integers(1, 129))
+        if not ops.mha_forward_supported(64 * h, h, l, torch.bfloat16):
+            continue
+        dtype = torch.bfloat16 if rng.random() < 0.7 else torch.float16
+        cases.append((int(rng.integers(1, 6)), l, h, dtype, bool(rng.random() < 0.5), bool(rng.random() < 0.3)))
+    return cases
+
+
+@pytest.mark.parametrize("b,l,h,dtype,causal,bias", _random_cases(24, 2024))
+def test_packed_random_shapes_against_the_oracle(cuda, b, l, h, dtype, causal, bias):
+    """The module's path (packed weights) against the float64 oracle on a
+    seeded sweep of supported shapes: every head count, lengths 1..128,
+    causal or not, biases, bf16 and fp16."""
+    run_case(cuda, b, l, h, dtype=dtype, causal=causal, bias=bias, seed=500 + l + 7 * h, packed=True)
 
 
 @pytest.mark.parametrize(
