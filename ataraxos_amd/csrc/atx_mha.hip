@@ -93,12 +93,12 @@ constexpr size_t mha_lds_o(int np) { return (size_t)16 * np * kD * 2; }
 // Y accumulated in registers across heads (H/2 feature tiles x np position
 // tiles per wave, at most 84 VGPRs) when the double-buffered O_h fits in LDS;
 // otherwise each head's O is parked in y and projected after the last head.
-// Measured on MI355X, the register form is slower for 4 heads at np = 4 and
-// for 8 heads at np <= 3 (the per-head Wo loads are exposed there), so those
-// park too.
+// Measured on MI355X, the register form is slower for 4 and 6 heads at
+// np = 4 and for 8 heads at np <= 3 (the per-head Wo loads are exposed
+// there), so those park too.
 constexpr bool mha_y_in_regs(int H, int np) {
     return (H / 2) * np * 4 <= 84 && mha_lds_core(64 * H, np) + 2 * mha_lds_o(np) <= kMhaLdsMax &&
-           !(H == 4 && np == 4) && !(H == 8 && np <= 3);
+           !((H == 4 || H == 6) && np == 4) && !(H == 8 && np <= 3);
 }
 inline size_t mha_lds_bytes(int E, int np) {
     return mha_lds_core(E, np) + (mha_y_in_regs(E / 64, np) ? 2 * mha_lds_o(np) : 0);
