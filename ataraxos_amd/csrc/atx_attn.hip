@@ -53,27 +53,39 @@ struct AttnArgs {
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 
-// Per-lane bitmask of usable keys (bit 4*kt + i <-> key 16*kt + 4*g + i):
-// inside the key range and not padded out.  The four padding bytes of one
-// (tile, lane group) are contiguous: one 4-byte load when the rows are 4-byte
-// aligned, else byte loads.
-__device__ inline uint64_t key_valid_bits(const AttnArgs& a, int b, int g, int nkt) {
-    uint64_t bits = 0;
+// Padding bytes of keys 4*lane .. 4*lane + 3 (byte i nonzero: key padded
+// out), one word per lane, so a wave covers S_kv <= 256.  A 4-byte load when
+// the rows are 4-byte aligned, else byte loads.  Issued before the K/V staging
+// loads, so its latency overlaps theirs.
+__device__ inline uint32_t key_pad_word(const AttnArgs& a, int b, int lane) {
     const uint8_t* row = a.kpad ? a.kpad + (int64_t)b * a.kpsb : nullptr;
-    for (int kt = 0; kt < nkt; ++kt) {
-        const int key0 = kt * 16 + 4 * g;
-        uint32_t pad = 0;  // byte i nonzero: key key0 + i is padded out
-        if (row && key0 < a.Skv) {
-            if (a.kpad_w4 && key0 + 4 <= a.Skv) {
-                pad = *reinterpret_cast<const uint32_t*>(row + key0);
-            } else {
-                for (int i = 0; i < 4; ++i)
-                    if (key0 + i < a.Skv) pad |= (uint32_t)row[key0 + i] << (8 * i);
-            }
+    const int key0 = 4 * lane;
+    uint32_t pad = 0;
+    if (row && key0 < a.Skv) {
+        if (a.kpad_w4 && key0 + 4 <= a.Skv) {
+            pad = *reinterpret_cast<const uint32_t*>(row + key0);
+        } else {
+            for (int i = 0; i < 4; ++i)
+                if (key0 + i < a.Skv) pad |= (uint32_t)row[key0 + i] << (8 * i);
         }
-        for (int i = 0; i < 4; ++i)
-            if (key0 + i < a.Skv && ((pad >> (8 * i)) & 0xff) == 0) bits |= (uint64_t)1 << (4 * kt + i);
     }
+    return pad;
+}
+
+// Per-lane bitmask of usable keys (bit 4*kt + i <-> key 16*kt + 4*g + i):
+// inside the key range and not padded out.  Ballot i has bit l set when key
+// 4l + i is usable; key 16kt + 4g + i is bit 4kt + g of ballot i.  Called by
+// the whole wave.
+template <int NKT>
+__device__ inline uint64_t key_valid_bits(const AttnArgs& a, int lane, int g, uint32_t pad) {
+    uint64_t bal[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bal[i] = __ballot(4 * lane + i < a.Skv && ((pad >> (8 * i)) & 0xffu) == 0);
+    uint64_t bits = 0;
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bits |= ((bal[i] >> (4 * kt + g)) & 1ull) << (4 * kt + i);
     return bits;
 }
 
@@ -112,7 +124,7 @@ constexpr int kOcc16[4][8][8] = {
         {8, 8, 8, 8, 7, 6, 5, 4},
         {8, 8, 7, 7, 6, 5, 5, 4},
         {8, 8, 7, 7, 6, 5, 5, 4},
-        {7, 7, 7, 6, 5, 5, 4, 4},
+        {7, 7, 6, 6, 5, 4, 4, 4},
         {6, 6, 6, 5, 5, 5, 4, 4},
         {5, 4, 4, 4, 4, 4, 4, 4},
     },
@@ -226,6 +238,8 @@ void attn_fwd_16bit(AttnArgs a) {
     u32x4 qop[NI];
     if (wave < nqt) load_q(wave, qop);
 
+    const uint32_t padw = MASKED ? key_pad_word(a, b, lane) : 0u;
+
     // ---- stage K and V rows 0 .. ROWS-1 (rows past S_kv read as zero:
     //      padded keys are masked by the -inf bias, padded values meet P = 0)
     u32x4 kreg[KIT], vreg[KIT];
@@ -257,7 +271,7 @@ void attn_fwd_16bit(AttnArgs a) {
     }
 
     uint64_t kbits = 0;
-    if constexpr (MASKED) kbits = key_valid_bits(a, b, g, NKT);
+    if constexpr (MASKED) kbits = key_valid_bits<NKT>(a, lane, g, padw);
     const float c2 = a.c2;
     const float kNegInf = -__builtin_inff();
     // Keys at or past S_kv can only sit in the last tile (S_kv > 16*(NKT-1)):
@@ -469,6 +483,7 @@ void attn_fwd_fp32(AttnArgs a) {
     const int m = lane & 15, g = lane >> 4;
     const int bh = blockIdx.x;
     const int b = bh / a.H, h = bh - b * a.H;
+    const uint32_t padw = key_pad_word(a, b, lane);  // loaded ahead of the staging (0 without a mask)
     const int hk = h / a.group;
 
     const float* kb = static_cast<const float*>(a.k) + b * a.ksb + hk * a.ksh;
@@ -498,7 +513,7 @@ void attn_fwd_fp32(AttnArgs a) {
     }
     const bool masked_path = a.causal || a.kpad != nullptr;
     uint64_t kbits = 0;
-    if (masked_path) kbits = key_valid_bits(a, b, g, nkt);
+    if (masked_path) kbits = key_valid_bits<NKT>(a, lane, g, padw);
     __syncthreads();
 
     const float c2 = a.c2;
