@@ -26,7 +26,19 @@ def _announce(msg: str) -> None:
     sys.stdout.flush()
 
 
-def run_case(cuda, b, sq, skv, h, hkv, d, dtype, causal=False, pad_p=None, seed=0, scale=None):
+def _on_gpu(pad, cuda, view):
+    """The padding mask on the GPU; with ``view``, as columns 1 .. skv of a
+    wider mask whose other columns are True, so that its rows start at odd
+    addresses with an odd stride (the kernels' byte-load path)."""
+    if not view:
+        return pad.to(cuda)
+    b, skv = pad.shape
+    big = torch.ones(b, skv + 3, dtype=torch.bool)
+    big[:, 1 : skv + 1] = pad
+    return big.to(cuda)[:, 1 : skv + 1]
+
+
+def run_case(cuda, b, sq, skv, h, hkv, d, dtype, causal=False, pad_p=None, seed=0, scale=None, pad_view=False):
     _announce(f"b={b} sq={sq} skv={skv} h={h} hkv={hkv} d={d} {dtype} causal={causal} pad={pad_p}")
     q = randn((b, sq, h, d), seed, dtype)
     k = randn((b, skv, hkv, d), seed + 1, dtype)
@@ -37,7 +49,7 @@ def run_case(cuda, b, sq, skv, h, hkv, d, dtype, causal=False, pad_p=None, seed=
         pad = torch.rand(b, skv, generator=g) < pad_p
     out = ops.attention_forward(
         q.to(cuda), k.to(cuda), v.to(cuda), causal=causal, scale=scale,
-        key_padding_mask=None if pad is None else pad.to(cuda),
+        key_padding_mask=None if pad is None else _on_gpu(pad, cuda, pad_view),
     )
     torch.cuda.synchronize()
     ref = oracle_attention(to_np64(q), to_np64(k), to_np64(v), causal=causal, scale=scale,
@@ -233,3 +245,10 @@ def test_large_logits_are_stable(cuda):
     assert torch.isfinite(out).all()
     ref = oracle_attention(to_np64(q), to_np64(k), to_np64(v))
     np.testing.assert_allclose(to_np64(out), ref, rtol=0, atol=1e-4 * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("skv,dtype,view", [(129, torch.bfloat16, False), (200, torch.float16, True), (256, torch.bfloat16, False), (256, torch.float32, True)])
+def test_key_padding_long_rows(cuda, skv, dtype, view):
+    """Key padding over 129..256 keys (every lane of the per-lane padding
+    words), with the mask rows 4-byte aligned or at odd addresses."""
+    run_case(cuda, 3, 48, skv, 4, 4, 64, dtype, pad_p=0.5, seed=600 + skv, pad_view=view)

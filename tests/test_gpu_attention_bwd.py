@@ -65,7 +65,19 @@ def inputs(b, sq, skv, h, d, dtype, seed, std=1.0):
     return q, k, v, g
 
 
-def run_case(cuda, b, sq, skv, h, d, dtype, causal=False, pad_p=None, seed=0, std=1.0, scale=None):
+def _on_gpu(pad, cuda, view):
+    """The padding mask on the GPU; with ``view``, as columns 1 .. skv of a
+    wider mask whose other columns are True, so that its rows start at odd
+    addresses with an odd stride (the kernels' byte-load path)."""
+    if not view:
+        return pad.to(cuda)
+    b, skv = pad.shape
+    big = torch.ones(b, skv + 3, dtype=torch.bool)
+    big[:, 1 : skv + 1] = pad
+    return big.to(cuda)[:, 1 : skv + 1]
+
+
+def run_case(cuda, b, sq, skv, h, d, dtype, causal=False, pad_p=None, seed=0, std=1.0, scale=None, pad_view=False):
     _announce(f"bwd b={b} sq={sq} skv={skv} h={h} d={d} {dtype} causal={causal} pad={pad_p} std={std}")
     q, k, v, g = inputs(b, sq, skv, h, d, dtype, seed, std)
     pad = None
@@ -73,7 +85,7 @@ def run_case(cuda, b, sq, skv, h, d, dtype, causal=False, pad_p=None, seed=0, st
         gen = torch.Generator().manual_seed(seed + 4)
         pad = torch.rand(b, skv, generator=gen) < pad_p
     qd, kd, vd, gd = (t.to(cuda) for t in (q, k, v, g))
-    padd = None if pad is None else pad.to(cuda)
+    padd = None if pad is None else _on_gpu(pad, cuda, pad_view)
     out = ops.attention_forward(qd, kd, vd, causal=causal, scale=scale, key_padding_mask=padd)
     dq, dk, dv = ops.attention_backward(qd, kd, vd, out, gd, causal=causal, scale=scale, key_padding_mask=padd)
     torch.cuda.synchronize()
@@ -276,3 +288,10 @@ def test_fp32_and_gqa_gradients_still_flow(cuda):
     out = ops.attention(qa, ka, ka)
     out.sum().backward()
     assert torch.isfinite(qa.grad).all() and torch.isfinite(ka.grad).all()
+
+
+@pytest.mark.parametrize("skv,dtype,view", [(129, torch.bfloat16, False), (200, torch.float16, True), (256, torch.bfloat16, True)])
+def test_key_padding_long_rows(cuda, skv, dtype, view):
+    """Backward with key padding over 129..256 keys (every lane of the
+    per-lane padding words), mask rows 4-byte aligned or at odd addresses."""
+    run_case(cuda, 3, 48, skv, 4, 64, dtype, pad_p=0.5, seed=700 + skv, pad_view=view)
