@@ -149,21 +149,6 @@ void attn_bwd_16bit(BwdArgs a) {
     };
     if (wave < nqt) load_o(wave);
 
-    // Padding bytes of keys 4*lane .. 4*lane + 3 (byte i nonzero: key padded
-    // out), one word per lane (S_kv <= 256), loaded ahead of the staging so
-    // that its latency overlaps the staging loads'.
-    const uint8_t* const prow = a.kpad ? a.kpad + (int64_t)b * a.kpsb : nullptr;
-    uint32_t padw = 0;
-    if (prow && 4 * lane < a.Skv) {
-        const int key0 = 4 * lane;
-        if ((reinterpret_cast<uintptr_t>(prow) & 3) == 0 && key0 + 4 <= a.Skv) {
-            padw = *reinterpret_cast<const uint32_t*>(prow + key0);
-        } else {
-            for (int i = 0; i < 4; ++i)
-                if (key0 + i < a.Skv) padw |= (uint32_t)prow[key0 + i] << (8 * i);
-        }
-    }
-
     // ---- stage K, V (RK rows), Q, dO (RQ rows) ------------------------------
     // Every load of a batch is issued before the first LDS store, so a
     // thread waits for memory once per batch (once in all at C3), not once
@@ -211,18 +196,21 @@ void attn_bwd_16bit(BwdArgs a) {
         lds_st4(sdelta + r * 4, 0u);
     }
 
-    // Usable keys (inside the range, not padded out): bit l of kbal[i] is key
-    // 4l + i.  Phase 1's per-lane bits (bit 4*kt + i <-> key 16*kt + 4g + i)
-    // are bit 4kt + g of kbal[i]; phase 2 tests its one key per lane the same
-    // way, with no memory access.
-    uint64_t kbal[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) kbal[i] = __ballot(4 * lane + i < a.Skv && ((padw >> (8 * i)) & 0xffu) == 0);
+    // Usable keys of this lane in phase 1 (bit 4*kt + i <-> key 16*kt + 4g + i).
     uint64_t kbits = 0;
 #pragma unroll
-    for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kbits |= ((kbal[i] >> (4 * kt + g)) & 1ull) << (4 * kt + i);
+    for (int kt = 0; kt < NKT; ++kt) {
+        const int n = min(max(a.Skv - (kt * 16 + 4 * g), 0), 4);
+        kbits |= (uint64_t)((1u << n) - 1u) << (4 * kt);
+    }
+    const uint8_t* prow = a.kpad ? a.kpad + (int64_t)b * a.kpsb : nullptr;
+    if (prow) {
+        for (int kt = 0; kt < NKT; ++kt)
+            for (int i = 0; i < 4; ++i) {
+                const int key = kt * 16 + 4 * g + i;
+                if (key < a.Skv && prow[key]) kbits &= ~((uint64_t)1 << (4 * kt + i));
+            }
+    }
     __syncthreads();
 
     // Per-lane LDS offsets.  Operand reads of 16-row tiles: row m, chunks
@@ -393,8 +381,7 @@ void attn_bwd_16bit(BwdArgs a) {
     for (int kt = wave; kt < NKT; kt += kWaves) {
         if (kt * 16 >= a.Skv) break;  // no key here: nothing to compute or store
         const int key = kt * 16 + m;
-        const uint64_t kb = (key & 2) ? ((key & 1) ? kbal[3] : kbal[2]) : ((key & 1) ? kbal[1] : kbal[0]);
-        const bool kok = (kb >> (key >> 2)) & 1ull;  // key < S_kv and not padded out
+        const bool kok = key < a.Skv && !(prow && prow[key]);
         const bool kfull = __builtin_amdgcn_ballot_w64(!kok) == 0;
         const lds_t* const kbase = sk + kt * 16 * RS;
         const lds_t* const vbase = sv + kt * 16 * RS;
