@@ -110,3 +110,20 @@ def test_decoder_self_attention_takes_the_fused_layer(cuda, monkeypatch):
     assert torch.equal(fused, direct)
     assert _rel(fused, unfused) <= 2e-2
     assert torch.isfinite(padded.float()).all()
+
+
+def test_decoder_self_attention_fused_sequence_first(cuda):
+    """batch_first=False: the fused layer reads the [S, B, E] input through a
+    transposed view and the result matches the batch-first module's."""
+    _announce("decoder self-attention fused, sequence first")
+    torch.manual_seed(4)
+    mb = use_hip_attention(torch.nn.MultiheadAttention(384, 6, batch_first=True)).to(cuda, torch.bfloat16).eval()
+    ms = use_hip_attention(torch.nn.MultiheadAttention(384, 6, batch_first=False)).to(cuda, torch.bfloat16).eval()
+    ms.load_state_dict(mb.state_dict())
+    x = torch.randn(5, 48, 384, device=cuda).bfloat16()
+    xs = x.transpose(0, 1).contiguous()
+    with torch.no_grad():
+        yb, _ = mb(x, x, x, need_weights=False)
+        ys, _ = ms(xs, xs, xs, need_weights=False)
+    assert ys.shape == (48, 5, 384)
+    assert torch.equal(ys.transpose(0, 1), yb)
