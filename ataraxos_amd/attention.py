@@ -20,7 +20,8 @@ Backends (``backend`` property, the slot of attention.py:122-146):
   Self-attention without autograd (inference, self-play) with head_dim 64,
   2/4/6/8 heads, no GQA, 16-bit and up to 128 positions runs the whole layer
   -- projections, attention, output projection -- as one launch
-  (``ops.mha_forward``) where that is faster, i.e. from the sequence length
+  (``ops.mha_forward``, weights rearranged into its tile order by one more
+  launch on every call) where that is faster, i.e. from the sequence length
   :data:`FUSED_MIN_SEQ` gives for the head count; with autograd the
   projections stay ``nn.Linear`` and the attention kernel's backward applies.
 * ``"math"`` — tensors on the CPU, or training with ``dropout > 0`` (the
@@ -39,7 +40,7 @@ import torch.nn.functional as F  # noqa: N812
 
 from . import ops
 
-__all__ = ["MultiHeadAttention", "math_attention", "packed_weights", "FUSED_MIN_SEQ"]
+__all__ = ["MultiHeadAttention", "math_attention", "FUSED_MIN_SEQ"]
 
 # Shortest sequence at which the one-launch layer (ops.mha_forward with packed
 # weights) beats the unfused path (hipBLASLt projections + the attention
@@ -49,26 +50,6 @@ __all__ = ["MultiHeadAttention", "math_attention", "packed_weights", "FUSED_MIN_
 # length, so the shortest sequences stay cheaper unfused: at 8 heads 158 us
 # fused against 116 us unfused at L=16, 191 against 198 at L=24.
 FUSED_MIN_SEQ = {2: 1, 4: 1, 6: 16, 8: 24}
-
-
-def packed_weights(
-    owner: nn.Module, sources: tuple[torch.Tensor, ...], ws: tuple[torch.Tensor, ...]
-) -> tuple[torch.Tensor, ...]:
-    """The ``[E, E]`` weights ``ws`` (views of the parameters ``sources``) in
-    the fused kernel's packed order (:func:`ops.mha_pack_weight`), cached on
-    ``owner`` (a plain attribute, not in the state_dict) under the identity,
-    address and version counter of ``sources``: replacing a parameter or
-    changing it in place (an optimizer step, ``load_state_dict``) makes the
-    next call repack.  Parameters created under ``torch.inference_mode()``
-    carry no version counter, so those are packed on every call."""
-    if any(t.is_inference() for t in sources):
-        return tuple(ops.mha_pack_weight(w.detach()) for w in ws)
-    key = tuple((id(t), t.data_ptr(), t._version, t.dtype) for t in sources)
-    cache = getattr(owner, "_packed", None)
-    if cache is None or cache[0] != key:
-        cache = (key, tuple(ops.mha_pack_weight(w.detach()) for w in ws))
-        owner._packed = cache
-    return cache[1]
 
 
 def math_attention(
@@ -141,11 +122,6 @@ class MultiHeadAttention(nn.Module):
         self.k_proj = nn.Linear(embed_dim, kv_dim, bias=qkv_bias)
         self.v_proj = nn.Linear(embed_dim, kv_dim, bias=qkv_bias)
         self.out_proj = nn.Linear(num_heads * self.head_dim, embed_dim, bias=qkv_bias)
-        # The fused layer reads the four weights in a packed tile order; the
-        # packed copies are kept here (not in the state_dict) with the key of
-        # the weights they were made from, and remade when a weight is
-        # replaced or changed in place (its version counter moves).
-        self._packed: tuple[tuple, tuple[torch.Tensor, ...]] | None = None
 
     @property
     def backend(self) -> str:
@@ -189,17 +165,18 @@ class MultiHeadAttention(nn.Module):
         w = self.q_proj.weight
         return x.dtype == w.dtype and ops.mha_forward_supported(self.embed_dim, self.num_heads, x.shape[1], x.dtype)
 
-    def _packed_weights(self) -> tuple[torch.Tensor, ...]:
-        """q/k/v/out_proj weights in the fused kernel's packed order, cached."""
-        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.out_proj.weight)
-        return packed_weights(self, ws, ws)
-
     def _forward_fused(self, x: torch.Tensor) -> torch.Tensor:
-        """Projections + attention + output projection in one kernel launch."""
+        """Projections + attention + output projection in one kernel launch,
+        after one launch that rearranges the four weights into the kernel's
+        tile order.  The rearrangement is redone on every call (a few
+        microseconds against the layer's hundreds), so weights changed in
+        place by any route -- an optimizer step, ``load_state_dict``, the
+        EMA swap's ``param.data.copy_`` -- are always the ones used."""
+        w = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.out_proj.weight)
         return ops.mha_forward(
-            x, *self._packed_weights(),
+            x, *(t.detach() for t in w),
             num_heads=self.num_heads, b_q=self.q_proj.bias, b_k=self.k_proj.bias, b_v=self.v_proj.bias,
-            b_o=self.out_proj.bias, causal=self.causal, scale=1.0 / math.sqrt(self.head_dim), packed=True,
+            b_o=self.out_proj.bias, causal=self.causal, scale=1.0 / math.sqrt(self.head_dim), repack=True,
         )
 
     def _expand_kv_heads(self, k: torch.Tensor, v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

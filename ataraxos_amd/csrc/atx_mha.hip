@@ -576,9 +576,9 @@ int dispatch_mha(int H, int np, int grid, size_t lds, hipStream_t st, const MhaA
 namespace atx {
 namespace {
 
-int mha_fwd(const AtxMhaParams* p, void* stream, bool packed) {
-    const char* const fn = packed ? "atx_mha_fwd_packed" : "atx_mha_fwd";
-    clear_error();
+// Validates `p` for entry point `fn` and fills the kernel arguments, the
+// position-tile count and the LDS size; no HIP call.
+int mha_check(const AtxMhaParams* p, const char* fn, MhaArgs& a, int& np, size_t& lds) {
     if (!p) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: params is NULL", fn);
     if (p->abi_version != ATX_ABI_VERSION)
         ATX_FAIL(ATX_ERR_ABI, "%s: abi_version %d, library is %d", fn, p->abi_version, ATX_ABI_VERSION);
@@ -591,6 +591,8 @@ int mha_fwd(const AtxMhaParams* p, void* stream, bool packed) {
     if (p->embed_dim != p->num_heads * 64)
         ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: head_dim %d not supported (64)", fn,
                  p->num_heads > 0 ? p->embed_dim / p->num_heads : 0);
+    if (p->num_heads != 2 && p->num_heads != 4 && p->num_heads != 6 && p->num_heads != 8)
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: %d heads not supported (2, 4, 6, 8)", fn, p->num_heads);
     if (!p->x || !p->w_q || !p->w_k || !p->w_v || !p->w_o || !p->y)
         ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: null tensor pointer", fn);
     if (!(p->scale > 0.f) || p->scale == __builtin_inff())
@@ -606,19 +608,21 @@ int mha_fwd(const AtxMhaParams* p, void* stream, bool packed) {
     if (xss < 0 || yss < E || (int64_t)(L + 16) * xss * 2 + E * 2 > 0x7fffffffLL ||
         (int64_t)(L + 16) * yss * 2 + E * 2 > 0x7fffffffLL)
         ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: row strides must be >= 0 (y: >= embed_dim) and one sample < 2 GiB", fn);
-    const int np = (L + 15) / 16;
-    const size_t lds = mha_lds_bytes(E, np);
+    np = (L + 15) / 16;
+    lds = mha_lds_bytes(E, np);
     if (lds > 160 * 1024)
         ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: seq %d, embed_dim %d need %zu bytes of LDS (> 160 KiB)", fn, L, E, lds);
 
-    MhaArgs a;
     a.x = p->x; a.xsb = p->x_stride_b; a.xss = (int)xss;
     a.w[0] = p->w_q; a.w[1] = p->w_k; a.w[2] = p->w_v; a.w[3] = p->w_o;
     a.bias[0] = p->b_q; a.bias[1] = p->b_k; a.bias[2] = p->b_v; a.bias[3] = p->b_o;
     a.y = p->y; a.ysb = p->y_stride_b; a.yss = (int)yss;
     a.L = L;
     a.c2 = p->scale * kLog2e;
-    hipStream_t st = static_cast<hipStream_t>(stream);
+    return ATX_OK;
+}
+
+int mha_launch(const AtxMhaParams* p, const MhaArgs& a, int np, size_t lds, hipStream_t st, bool packed) {
     const int H = p->num_heads;
     const bool bf = p->dtype == ATX_DTYPE_BF16;
     if (packed) {
@@ -633,6 +637,16 @@ int mha_fwd(const AtxMhaParams* p, void* stream, bool packed) {
                      : dispatch_mha<_Float16, false, false>(H, np, p->batch, lds, st, a);
 }
 
+int mha_fwd(const AtxMhaParams* p, void* stream, bool packed) {
+    const char* const fn = packed ? "atx_mha_fwd_packed" : "atx_mha_fwd";
+    clear_error();
+    MhaArgs a;
+    int np = 0;
+    size_t lds = 0;
+    if (const int rc = mha_check(p, fn, a, np, lds)) return rc;
+    return mha_launch(p, a, np, lds, static_cast<hipStream_t>(stream), packed);
+}
+
 // Packed tile order of one [E, E] weight (see wtile_off): thread i writes
 // 16-byte chunk i of the packed matrix.
 __global__ __launch_bounds__(256) void mha_pack_weight(const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int E) {
@@ -645,12 +659,81 @@ __global__ __launch_bounds__(256) void mha_pack_weight(const uint16_t* __restric
     st16(out + (size_t)i * 8, ld16(w + (size_t)(rt * 16 + m) * E + kt * 32 + g * 8));
 }
 
+// The four weights of a layer into consecutive packed [E, E] matrices in one
+// launch (blockIdx.y = q, k, v, out).
+struct Pack4Args {
+    const uint16_t* w[4];
+    uint16_t* out;
+    int E;
+};
+__global__ __launch_bounds__(256) void mha_pack_weights4(Pack4Args a) {
+    const int which = blockIdx.y;
+    const uint16_t* const w = which == 0 ? a.w[0] : which == 1 ? a.w[1] : which == 2 ? a.w[2] : a.w[3];
+    const int E = a.E;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int ks = E / 32;
+    if (i >= E * ks * 4) return;
+    const int lane = i & 63, t = i >> 6;
+    const int kt = t % ks, rt = t / ks;
+    const int m = lane & 15, g = lane >> 4;
+    st16(a.out + (size_t)which * E * E + (size_t)i * 8, ld16(w + (size_t)(rt * 16 + m) * E + kt * 32 + g * 8));
+}
+
+inline bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + nb && y < x + na;
+}
+
+// Body of atx_mha_fwd_ws: validate, check the
+// workspace against the layer, pack the four row-major weights into it (one
+// launch), run the packed-order kernel from it.
+int mha_fwd_repack(const AtxMhaParams* p, void* ws, int64_t ws_bytes, hipStream_t st, const char* fn) {
+    MhaArgs a;
+    int np = 0;
+    size_t lds = 0;
+    if (const int rc = mha_check(p, fn, a, np, lds)) return rc;
+    const int E = p->embed_dim;
+    const size_t mat = (size_t)E * E * 2, need = 4 * mat;
+    if (!ws) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: workspace is NULL", fn);
+    if (reinterpret_cast<uintptr_t>(ws) & 255) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: workspace must be 256-byte aligned", fn);
+    if (ws_bytes < 0 || (size_t)ws_bytes < need)
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: workspace of %lld bytes, embed_dim %d needs %zu", fn, (long long)ws_bytes, E,
+                 need);
+    const void* const w[4] = {p->w_q, p->w_k, p->w_v, p->w_o};
+    for (int i = 0; i < 4; ++i)
+        if (overlaps(ws, need, w[i], mat)) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: workspace overlaps a weight", fn);
+    // extents of x and y (first to last element touched, strides >= 0)
+    const auto extent = [&](int64_t sb, int64_t ss) {
+        return (size_t)(((int64_t)(p->batch - 1) * (sb > 0 ? sb : 0) + (int64_t)(p->seq - 1) * ss + E) * 2);
+    };
+    if (overlaps(ws, need, p->x, extent(p->x_stride_b, a.xss)) || overlaps(ws, need, p->y, extent(p->y_stride_b, a.yss)))
+        ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: workspace overlaps x or y", fn);
+    Pack4Args pa;
+    for (int i = 0; i < 4; ++i) pa.w[i] = static_cast<const uint16_t*>(w[i]);
+    pa.out = static_cast<uint16_t*>(ws);
+    pa.E = E;
+    const int chunks = E * E / 8;
+    hipLaunchKernelGGL(mha_pack_weights4, dim3((chunks + 255) / 256, 4), dim3(256), 0, st, pa);
+    ATX_CHECK_LAUNCH("atx_mha pack launch");
+    for (int i = 0; i < 4; ++i) a.w[i] = static_cast<const char*>(ws) + i * mat;
+    return mha_launch(p, a, np, lds, st, true);
+}
+
 }  // namespace
 }  // namespace atx
 
 extern "C" int atx_mha_fwd(const AtxMhaParams* p, void* stream) { return atx::mha_fwd(p, stream, false); }
 
 extern "C" int atx_mha_fwd_packed(const AtxMhaParams* p, void* stream) { return atx::mha_fwd(p, stream, true); }
+
+extern "C" int64_t atx_mha_workspace_bytes(int32_t embed_dim) {
+    return embed_dim > 0 ? 4 * (int64_t)embed_dim * embed_dim * 2 : 0;
+}
+
+extern "C" int atx_mha_fwd_ws(const AtxMhaParams* p, void* workspace, int64_t workspace_bytes, void* stream) {
+    atx::clear_error();
+    return atx::mha_fwd_repack(p, workspace, workspace_bytes, static_cast<hipStream_t>(stream), "atx_mha_fwd_ws");
+}
 
 extern "C" int atx_mha_pack_weight(int dtype, int dim, const void* w, void* packed, void* stream) {
     using namespace atx;

@@ -93,6 +93,13 @@ class SetupDecoder:
     def __init__(self, net: torch.nn.Module, batch: int, capacity: int = 40) -> None:
         self.net = net
         blocks = list(net.blocks.blocks)
+        not_causal = [i for i, blk in enumerate(blocks) if not getattr(blk.attn, "causal", False)]
+        if not_causal:
+            # SetupNetwork(causal=False) is a valid reference configuration
+            # (setup_net.py:78,95), but then position t sees later tokens and
+            # a KV-cache decode is not the full-prefix recompute.
+            raise ValueError(f"SetupDecoder: blocks {not_causal} are not causal; token-by-token decoding "
+                             "equals the full recompute only for a causal network")
         attn = blocks[0].attn
         p = next(net.parameters())
         self.heads, self.kv_heads, self.head_dim = attn.num_heads, attn.num_kv_heads, attn.head_dim
@@ -151,9 +158,14 @@ class BeliefDecoder:
     def __init__(self, net: torch.nn.Module, infostate: torch.Tensor, hidden_mask: torch.Tensor,
                  capacity: int = 40) -> None:
         self.net = net
+        self.layers = list(net.decoder.layers)
+        not_pre_ln = [i for i, layer in enumerate(self.layers) if not getattr(layer, "norm_first", False)]
+        if not_pre_ln:
+            # _row applies norm1/norm2/norm3 before each sublayer, the order of
+            # norm_first=True (belief_net.py:105-114).
+            raise ValueError(f"BeliefDecoder: decoder layers {not_pre_ln} are not norm_first (pre-LN)")
         with torch.no_grad():
             enc = net(infostate, hidden_mask)  # [B, 100, dim]: target_tokens None -> encoder output
-        self.layers = list(net.decoder.layers)
         first = self.layers[0].self_attn
         self.dim, self.heads = first.embed_dim, first.num_heads
         self.head_dim = self.dim // self.heads

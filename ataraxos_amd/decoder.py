@@ -24,7 +24,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
-from .attention import FUSED_MIN_SEQ, packed_weights
+from .attention import FUSED_MIN_SEQ
 
 __all__ = ["KernelMultiheadAttention", "use_hip_attention"]
 
@@ -43,7 +43,8 @@ class KernelMultiheadAttention(nn.MultiheadAttention):
     Self-attention (``query``, ``key`` and ``value`` the same tensor, as
     ``TransformerDecoderLayer`` calls it) without a key padding mask and
     without autograd runs as one launch of the fused layer
-    (``ops.mha_forward``, packed weights cached on the module) where that is
+    (``ops.mha_forward``, weights rearranged into its tile order on every
+    call) where that is
     faster (``FUSED_MIN_SEQ``, head_dim 64); ``fuse_layer = False`` keeps the
     projections + attention kernel path.
     """
@@ -92,9 +93,9 @@ class KernelMultiheadAttention(nn.MultiheadAttention):
             assert self.in_proj_weight is not None
             ws = (w_q, w_k, w_v, self.out_proj.weight)
             out = ops.mha_forward(
-                query, *packed_weights(self, (self.in_proj_weight, self.out_proj.weight), ws),
+                query, *(t.detach() for t in ws),
                 num_heads=h, b_q=b_q, b_k=b_k, b_v=b_v, b_o=self.out_proj.bias, causal=is_causal,
-                scale=d**-0.5, packed=True,
+                scale=d**-0.5, repack=True,
             )
             return (out if self.batch_first else out.transpose(0, 1)), None
         q = F.linear(query, w_q, b_q).view(b, sq, h, d)

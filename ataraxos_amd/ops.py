@@ -22,6 +22,7 @@ outside the kernels' range raises.
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -51,13 +52,35 @@ def _require_device(name: str, *tensors: torch.Tensor) -> None:
             raise RuntimeError(f"{name}: tensors on different devices ({dev} vs {t.device})")
 
 
-def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
-    """Return ``t`` (or a contiguous copy) so that every row of its last dim
-    is contiguous and starts on a 16-byte boundary, as the kernels require."""
+def _rows_ok(t: torch.Tensor) -> bool:
+    """Every row of the last dim is contiguous and starts on a 16-byte boundary."""
     es = t.element_size()
-    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0
-    ok = ok and all((s * es) % 16 == 0 for s in t.stride()[:-1])
-    return t if ok else t.contiguous()
+    return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+            and all((s * es) % 16 == 0 for s in t.stride()[:-1]))
+
+
+def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
+    """Return ``t`` or a copy of it whose rows of the last dim are contiguous
+    and start on 16-byte boundaries, as the kernels require.  A contiguous
+    view at a misaligned address (``contiguous()`` returns it unchanged) is
+    copied into a fresh allocation."""
+    if _rows_ok(t):
+        return t
+    c = t.contiguous()
+    if not _rows_ok(c):
+        c = t.clone(memory_format=torch.contiguous_format)
+    return c
+
+
+def _check_out(name: str, out: torch.Tensor, shape: tuple, dtype: torch.dtype, device: torch.device) -> None:
+    """A caller-supplied output must have exactly ``shape``, ``dtype`` and
+    ``device``, a contiguous last dim and 16-byte aligned rows: the ABI
+    passes no stride for the last dim and sizes its bounds from the strides."""
+    if tuple(out.shape) != tuple(shape) or out.dtype != dtype or out.device != device:
+        raise ValueError(f"{name}: out must be {tuple(shape)} {dtype} on {device}, "
+                         f"got {tuple(out.shape)} {out.dtype} on {out.device}")
+    if not _rows_ok(out):
+        raise ValueError(f"{name}: out needs a contiguous last dim and 16-byte aligned rows")
 
 
 def _padding_bytes(key_padding_mask: torch.Tensor | None, b: int, skv: int, ref: torch.Tensor):
@@ -105,8 +128,8 @@ def attention_forward(
     q, k, v = _aligned_rows(q), _aligned_rows(k), _aligned_rows(v)
     if out is None:
         out = torch.empty((b, sq, h, d), dtype=q.dtype, device=q.device)
-    elif tuple(out.shape) != (b, sq, h, d) or out.dtype != q.dtype or out.device != q.device:
-        raise ValueError("attention: out has the wrong shape, dtype or device")
+    else:
+        _check_out("attention", out, (b, sq, h, d), q.dtype, q.device)
     pad = _padding_bytes(key_padding_mask, b, skv, q)
     if scale is None:
         scale = 1.0 / math.sqrt(d)
@@ -437,6 +460,8 @@ def mha_forward(
     scale: float | None = None,
     out: torch.Tensor | None = None,
     packed: bool = False,
+    repack: bool = False,
+    workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Whole self-attention layer in one launch (no autograd):
     ``out_proj(attention(q_proj(x), k_proj(x), v_proj(x)))`` with the
@@ -444,9 +469,16 @@ def mha_forward(
     -> ``[B, L, E]`` in x's dtype.  Q, K, V and the attention output are
     rounded to x's dtype, as the reference's bf16 modules round them.
 
-    ``packed=True``: the four weights are the outputs of
-    :func:`mha_pack_weight` (``atx_mha_fwd_packed``, the faster kernel;
-    identical results)."""
+    Weight orders (identical results):
+
+    * default: the ``nn.Linear`` matrices, read as they are (``atx_mha_fwd``);
+    * ``packed=True``: the outputs of :func:`mha_pack_weight`
+      (``atx_mha_fwd_packed``, the faster kernel);
+    * ``repack=True``: the ``nn.Linear`` matrices, rearranged into
+      ``workspace`` (a uint8 device tensor of at least
+      :func:`mha_workspace_bytes` bytes, allocated here when None) by one
+      extra launch on every call, then the packed kernel (``atx_mha_fwd_ws``).
+      What the modules use: no cached copy can go stale."""
     _require_device("mha_forward", x, w_q, w_k, w_v, w_o)
     if x.dim() != 3:
         raise ValueError("mha_forward: x must be [batch, seq, embed_dim]")
@@ -466,12 +498,14 @@ def mha_forward(
             _require_device("mha_forward", x, t)
             t = t.contiguous()
         biases.append(t)
+    if packed and repack:
+        raise ValueError("mha_forward: packed and repack are exclusive")
     x = _aligned_rows(x)
-    ws = [w.contiguous() if not w.is_contiguous() or w.data_ptr() % 16 else w for w in (w_q, w_k, w_v, w_o)]
+    ws = [_aligned_rows(w) if w.is_contiguous() else _aligned_rows(w.contiguous()) for w in (w_q, w_k, w_v, w_o)]
     if out is None:
         out = torch.empty((b, l, e), dtype=x.dtype, device=x.device)
-    elif tuple(out.shape) != (b, l, e) or out.dtype != x.dtype or out.stride(-1) != 1:
-        raise ValueError("mha_forward: out has the wrong shape, dtype or layout")
+    else:
+        _check_out("mha_forward", out, (b, l, e), x.dtype, x.device)
     if scale is None:
         scale = 1.0 / 8.0  # 1 / sqrt(head_dim = 64)
 
@@ -485,9 +519,25 @@ def mha_forward(
     p.b_q, p.b_k, p.b_v, p.b_o = (t.data_ptr() if t is not None else None for t in biases)
     p.y, p.y_stride_b, p.y_stride_s = out.data_ptr(), out.stride(0), out.stride(1)
     p.scale = float(scale)
+    if repack:
+        need = mha_workspace_bytes(e)
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+        elif (workspace.dtype != torch.uint8 or workspace.device != x.device or not workspace.is_contiguous()
+              or workspace.numel() < need):
+            raise ValueError(f"mha_forward: workspace must be a contiguous uint8 tensor of >= {need} bytes on {x.device}")
+        rc = _lib.load().atx_mha_fwd_ws(ctypes.byref(p), workspace.data_ptr(), workspace.numel(), _stream(x))
+        _lib.check(rc, "atx_mha_fwd_ws")
+        return out
     name = "atx_mha_fwd_packed" if packed else "atx_mha_fwd"
     _lib.check(_lib.call(name, p, _stream(x)), name)
     return out
+
+
+def mha_workspace_bytes(embed_dim: int) -> int:
+    """Bytes of the workspace of ``mha_forward(..., repack=True)``: the four
+    weights in the packed order (``atx_mha_workspace_bytes``)."""
+    return 4 * embed_dim * embed_dim * 2
 
 
 def mha_pack_weight(w: torch.Tensor) -> torch.Tensor:
@@ -545,6 +595,8 @@ def attention_decode(
         k_new, v_new = _aligned_rows(k_new), _aligned_rows(v_new)
     if out is None:
         out = torch.empty((b, h, d), dtype=q.dtype, device=q.device)
+    else:
+        _check_out("attention_decode", out, (b, h, d), q.dtype, q.device)
     if scale is None:
         scale = 1.0 / math.sqrt(d)
 

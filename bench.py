@@ -48,6 +48,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -73,7 +74,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--qkv", choices=("separate", "packed"), default="separate",
                     help="q/k/v as three tensors or as views of one fused [B, L, 3E] projection")
     ap.add_argument("--no-extras", action="store_true", help="skip the e2e, kq_policy, belief_attention, decode, backward and rollout legs")
-    ap.add_argument("--cpu-sample", type=int, default=1024, help="batch of the CPU baseline sample")
+    ap.add_argument("--cpu-sample", type=int, default=4096, help="batch of the C3 CPU baseline sample")
     ap.add_argument(
         "--mode",
         choices=("bench", "pmc"),
@@ -163,14 +164,21 @@ def make_layers(torch, batch, seq, embed, layers, dev, packed=False):
 
 
 def time_attention(torch, ops, layers, heads, head_dim, steps, warmup):
-    """Time `steps` passes over all layers; return (ms_per_step, mean kernel ms)."""
+    """Time `steps` passes over all layers after `warmup` untimed passes and
+    at least ``SETTLE_MS`` of continuous untimed passes (the clocks' ramp, so
+    the timed region sees the steady state whatever `warmup` is).  Returns
+    (ms_per_step, per-launch kernel ms: mean, median, min)."""
     b, l, e = layers[0][0].shape
     views = [tuple(t.unflatten(-1, (heads, head_dim)) for t in qkv) for qkv in layers]
     outs = [torch.empty(b, l, heads, head_dim, dtype=torch.bfloat16, device=layers[0][0].device) for _ in layers]
-    for _ in range(warmup):
+
+    def one_pass():
         for (q, k, v), o in zip(views, outs):
             ops.attention_forward(q, k, v, out=o)
-    torch.cuda.synchronize()
+
+    for _ in range(warmup):
+        one_pass()
+    _settle(torch, one_pass)
     n = steps * len(views)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
     start = torch.cuda.Event(enable_timing=True)
@@ -188,7 +196,7 @@ def time_attention(torch, ops, layers, heads, head_dim, steps, warmup):
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(stop)
     per_launch = [ev[j].elapsed_time(ev[j + 1]) for j in range(n)]
-    return total_ms / steps, sum(per_launch) / len(per_launch), min(per_launch)
+    return total_ms / steps, sum(per_launch) / len(per_launch), statistics.median(per_launch), min(per_launch)
 
 
 def time_e2e(torch, batch, seq, embed, heads, layers_n, steps, warmup, dev, fuse=True):
@@ -485,20 +493,40 @@ def time_rollout(torch, dev, steps, warmup):
 
 
 def cpu_baseline(sample: int) -> dict:
-    from oracle.cpu_baseline import attention_baseline
+    """The reference's math path timed with torch on the host CPU (fp32 on
+    bf16-rounded inputs, 3 warm-ups, median of <= 10 runs): C3 at the
+    benchmark batch (``value``), C1 at B=64 and the C2 policy softmax at
+    B=4096.  Threads: the box's CPU share (OMP_NUM_THREADS, 16 on the GPU
+    boxes), capped by os.cpu_count()."""
+    from oracle.cpu_baseline import attention_baseline, kq_baseline
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
     threads = min(threads, os.cpu_count() or threads)
-    r = attention_baseline(sample, 100, 6, 64, threads)
+    c3 = attention_baseline(sample, 100, 6, 64, threads)
+    c1 = attention_baseline(64, 100, 6, 64, threads, seed=42)
+    c2 = kq_baseline(4096, 100, 64, threads)
+
+    def leg(r, what, batch, nbytes, flops):
+        t = r["seconds_per_call"]
+        return {"what": what, "batch": batch, "samples_per_s": batch / t, "ms_per_call": t * 1e3,
+                "gbs": batch * nbytes / t / 1e9, "tflops": batch * flops / t / 1e12, "runs": r["runs"]}
+
     return {
-        "value": r["samples_per_s"],
+        "value": c3["samples_per_s"],
         "unit": "samples/s",
-        "cores": threads,
+        "cores": c3["torch_threads"],
         "kind": "port",
-        "sample": (
-            f"B={sample} of the C3 layer (L=100, 6x64) through the reference math path "
-            f"(torch fp32 on bf16-rounded inputs, {r['cpu_model']}), median of <=10 runs after 3 warm-ups"
-        ),
+        "sample": f"C3 self-attention core, B={sample}, L=100, 6x64, torch fp32 math path on the host CPU",
+        "cpu_model": c3["cpu_model"],
+        "os_cpu_count": c3["os_cpu_count"],
+        "torch_threads": c3["torch_threads"],
+        "legs": {
+            "C3": leg(c3, "attention core, B=%d, L=100, 6x64" % sample, sample, 4 * 100 * 384 * 4,
+                      4 * 6 * 100 * 100 * 64),
+            "C1": leg(c1, "attention core, B=64, L=100, 6x64 (config 1)", 64, 4 * 100 * 384 * 4, 4 * 6 * 100 * 100 * 64),
+            "C2": leg(c2, "policy logits + legal mask + softmax over 10^4, B=4096, d=64", 4096,
+                      2 * 100 * 64 * 4 + 100 * 100 + 100 * 100 * 4, 2 * 100 * 100 * 64),
+        },
     }
 
 
@@ -529,13 +557,16 @@ def main() -> int:
     torch.cuda.synchronize()
     print(f"[bench] inputs ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
 
-    ms_step, kern_ms, kern_min_ms = time_attention(torch, ops, layers, heads, head_dim, args.steps, args.warmup)
+    ms_step, kern_mean_ms, kern_ms, kern_min_ms = time_attention(
+        torch, ops, layers, heads, head_dim, args.steps, args.warmup)
     del layers
-    print(f"[bench] attention timed: {ms_step:.3f} ms/step, {kern_ms * 1e3:.1f} us/launch", file=sys.stderr, flush=True)
+    print(f"[bench] attention timed: {ms_step:.3f} ms/step, {kern_ms * 1e3:.1f} us/launch (median)",
+          file=sys.stderr, flush=True)
 
     bytes_per_sample = 4 * seq * embed * 2  # Q, K, V read + O written, bf16
     flops_per_sample = 4 * heads * seq * seq * head_dim
     value = args.layers * batch / (ms_step * 1e-3)
+    # roofline from the median launch (BASELINE's GPU method: median of >= 50)
     achieved = batch * bytes_per_sample / (kern_ms * 1e-3) / 1e9
     tflops = batch * flops_per_sample / (kern_ms * 1e-3) / 1e12
     traffic = None
@@ -577,8 +608,10 @@ def main() -> int:
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic,
             "kernel": "attn_fwd_16bit<bf16, D=64, NKC=4>",
-            "kernel_us_mean": kern_ms * 1e3,
+            "kernel_us_median": kern_ms * 1e3,
+            "kernel_us_mean": kern_mean_ms * 1e3,
             "kernel_us_min": kern_min_ms * 1e3,
+            "launches_timed": args.steps * args.layers,
             "algorithmic_bytes_per_launch": batch * bytes_per_sample,
         },
         "mfma": {
@@ -593,7 +626,7 @@ def main() -> int:
         unf_ms = time_e2e(torch, batch, seq, embed, heads, args.layers, max(5, args.steps // 5), 3, dev, fuse=False)
         layer_flops = batch * (4 * 2 * seq * embed * embed + heads * 2 * 2 * seq * seq * (embed // heads))
         result["e2e"] = {
-            "what": "MultiHeadAttention forward x8 + residual, each layer one launch of the fused layer kernel (weights packed once per weight update, cached by the module)",
+            "what": "MultiHeadAttention forward x8 + residual as the module runs it in inference: per layer one launch rearranging the four weights into the fused kernel's tile order, one launch of the fused layer",
             "ms_per_step": e2e_ms,
             "samples_per_s": batch / (e2e_ms * 1e-3),
             "mfma_tflops": args.layers * layer_flops / (e2e_ms * 1e-3) / 1e12,

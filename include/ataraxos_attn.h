@@ -308,6 +308,25 @@ int atx_mha_fwd_packed(const AtxMhaParams* params, void* stream);
  */
 int atx_mha_pack_weight(int32_t dtype, int32_t dim, const void* w, void* packed, void* stream);
 
+/* Bytes of the workspace atx_mha_fwd_ws needs at this embed_dim: the four
+ * weights in the packed tile order, 4 * embed_dim^2 * 2 (0 if embed_dim < 1). */
+int64_t atx_mha_workspace_bytes(int32_t embed_dim);
+
+/*
+ * atx_mha_fwd with the weights in the nn.Linear order (as atx_mha_fwd takes
+ * them), run through the packed-order kernel: one launch rearranges all four
+ * weights into `workspace` (the layout of atx_mha_pack_weight, q, k, v, out
+ * consecutively), a second runs the layer from there.  Results are identical
+ * to atx_mha_fwd and atx_mha_fwd_packed.  `workspace`: device memory of at
+ * least atx_mha_workspace_bytes(embed_dim) bytes, 256-byte aligned, not
+ * overlapping x, y or a weight; its contents are overwritten.  Because the
+ * weights are rearranged on every call, an in-place change of a weight
+ * (optimizer step, EMA swap through param.data.copy_) is always seen.
+ * Replaces the same reference lines as atx_mha_fwd
+ * (stratego/networks/attention.py:152-204 with key_value = None).
+ */
+int atx_mha_fwd_ws(const AtxMhaParams* params, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Single-query attention over a KV cache (incremental decode)              */
 /* ------------------------------------------------------------------------ */

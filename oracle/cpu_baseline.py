@@ -53,9 +53,10 @@ def cpu_info() -> dict:
     return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads()}
 
 
-def time_fn(fn, warmup: int = 3, reps: int = 10, budget_s: float = 20.0) -> float:
+def time_fn(fn, warmup: int = 3, reps: int = 10, budget_s: float = 20.0) -> tuple[float, int]:
     """Median wall time of ``fn()`` over up to ``reps`` runs after ``warmup``,
-    stopping early once ``budget_s`` seconds have been spent."""
+    stopping early once ``budget_s`` seconds have been spent; returns
+    (median seconds, runs timed)."""
     for _ in range(warmup):
         fn()
     times: list[float] = []
@@ -66,7 +67,7 @@ def time_fn(fn, warmup: int = 3, reps: int = 10, budget_s: float = 20.0) -> floa
         times.append(time.perf_counter() - t0)
         if time.perf_counter() - start > budget_s and len(times) >= 3:
             break
-    return statistics.median(times)
+    return statistics.median(times), len(times)
 
 
 def attention_baseline(batch: int, seq: int, heads: int, head_dim: int, threads: int, seed: int = 45) -> dict:
@@ -76,8 +77,8 @@ def attention_baseline(batch: int, seq: int, heads: int, head_dim: int, threads:
     shape = (batch, seq, heads, head_dim)
     q, k, v = (torch.randn(shape, generator=g).bfloat16().float() for _ in range(3))
     with torch.inference_mode():
-        t = time_fn(lambda: math_attention_cpu(q, k, v))
-    return {"seconds_per_call": t, "samples_per_s": batch / t, **cpu_info()}
+        t, runs = time_fn(lambda: math_attention_cpu(q, k, v))
+    return {"seconds_per_call": t, "samples_per_s": batch / t, "runs": runs, **cpu_info()}
 
 
 def kq_baseline(batch: int, seq: int, dim: int, threads: int, seed: int = 44) -> dict:
@@ -86,6 +87,7 @@ def kq_baseline(batch: int, seq: int, dim: int, threads: int, seed: int = 44) ->
     q = torch.randn(batch, seq, dim, generator=g).bfloat16().float()
     k = torch.randn(batch, seq, dim, generator=g).bfloat16().float()
     mask = torch.rand(batch, seq, seq, generator=g) < 0.02
+    mask[:, 0, 0] |= ~mask.flatten(1).any(dim=1)  # >= 1 legal entry per sample (config 2)
     with torch.inference_mode():
-        t = time_fn(lambda: kq_probs_cpu(q, k, mask, 1.0 / math.sqrt(dim)))
-    return {"seconds_per_call": t, "samples_per_s": batch / t, **cpu_info()}
+        t, runs = time_fn(lambda: kq_probs_cpu(q, k, mask, 1.0 / math.sqrt(dim)))
+    return {"seconds_per_call": t, "samples_per_s": batch / t, "runs": runs, **cpu_info()}

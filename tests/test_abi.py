@@ -274,6 +274,82 @@ def test_fused_layer_validation_codes():
     _expect("atx_mha_fwd_packed", p, _lib.ERR_UNSUPPORTED, "LDS")
 
 
+def test_workspace_entry_point_validation_codes():
+    """atx_mha_fwd_ws validates the layer as atx_mha_fwd does, then the
+    workspace (size, alignment, overlap), all before any HIP call."""
+    lib = _lib.load()
+    p = _lib.MhaParams()
+    p.abi_version, p.dtype, p.batch, p.seq, p.embed_dim, p.num_heads = _lib.ABI_VERSION, _lib.DTYPE_BF16, 4, 100, 384, 6
+    x, y = 1 << 30, 2 << 30
+    p.x, p.y = x, y
+    p.w_q, p.w_k, p.w_v, p.w_o = ((3 << 30) + i * (1 << 20) for i in range(4))
+    p.x_stride_b = p.y_stride_b = 100 * 384
+    p.x_stride_s = p.y_stride_s = 384
+    p.scale = 0.125
+    need = lib.atx_mha_workspace_bytes(384)
+    assert need == 4 * 384 * 384 * 2 and lib.atx_mha_workspace_bytes(0) == 0
+    ws = 4 << 30
+
+    def expect(work, nbytes, code, text):
+        rc = lib.atx_mha_fwd_ws(ctypes.byref(p), work, nbytes, None)
+        assert rc == code, (rc, _lib.last_error())
+        assert text in _lib.last_error() and "atx_mha_fwd_ws" in _lib.last_error()
+
+    expect(None, need, _lib.ERR_INVALID_ARGUMENT, "NULL")
+    expect(ws + 16, need, _lib.ERR_INVALID_ARGUMENT, "256-byte")
+    expect(ws, need - 1, _lib.ERR_INVALID_ARGUMENT, "needs")
+    expect(int(p.w_k) - 1024, need, _lib.ERR_INVALID_ARGUMENT, "overlaps a weight")
+    expect(y + 4 * 100 * 384 * 2 - 256, need, _lib.ERR_INVALID_ARGUMENT, "overlaps x or y")
+    expect(x - need + 256, need, _lib.ERR_INVALID_ARGUMENT, "overlaps x or y")
+    p.seq = 129  # the layer itself is checked first
+    expect(ws, need, _lib.ERR_UNSUPPORTED, "seq")
+    assert lib.atx_mha_fwd_ws(None, ws, need, None) == _lib.ERR_INVALID_ARGUMENT
+
+
+def test_output_and_alignment_helpers():
+    """ops._check_out refuses outputs the ABI cannot describe (wrong shape or
+    dtype, a strided last dim, misaligned rows); ops._aligned_rows copies a
+    contiguous view that starts at a misaligned address."""
+    from ataraxos_amd import ops
+
+    dev = torch.device("cpu")
+    good = torch.empty(2, 3, 4, 16, dtype=torch.bfloat16)
+    ops._check_out("t", good, (2, 3, 4, 16), torch.bfloat16, dev)
+    for bad, text in [
+        (torch.empty(2, 3, 4, 8, dtype=torch.bfloat16), "out must be"),
+        (torch.empty(2, 3, 4, 16, dtype=torch.float32), "out must be"),
+        (torch.empty(2, 3, 4, 32, dtype=torch.bfloat16)[..., ::2], "contiguous last dim"),
+        (torch.empty(2 * 3 * 4 * 16 + 1, dtype=torch.bfloat16)[1:].view(2, 3, 4, 16), "16-byte"),
+    ]:
+        with pytest.raises(ValueError, match=text):
+            ops._check_out("t", bad, (2, 3, 4, 16), torch.bfloat16, dev)
+    base = torch.arange(1 + 4 * 64, dtype=torch.bfloat16)
+    mis = base[1:].view(4, 64)
+    assert mis.is_contiguous() and mis.data_ptr() % 16 != 0
+    fixed = ops._aligned_rows(mis)
+    assert fixed.data_ptr() % 16 == 0 and torch.equal(fixed, mis)
+    strided = torch.arange(4 * 128, dtype=torch.bfloat16).view(4, 128)[:, ::2]
+    fixed = ops._aligned_rows(strided)
+    assert fixed.stride(-1) == 1 and torch.equal(fixed, strided)
+    assert ops._aligned_rows(good) is good
+
+
+def test_decoders_refuse_networks_they_do_not_restate():
+    """SetupDecoder needs causal blocks; BeliefDecoder needs pre-LN decoder
+    layers (its per-row step applies the norms first)."""
+    from ataraxos_amd import BeliefDecoder, SetupDecoder
+    from tests._netlike import BeliefLike, SetupLike
+
+    net = SetupLike(depth=2, dim=64, heads=2, ff=64)
+    net.blocks.blocks[1].attn.causal = False
+    with pytest.raises(ValueError, match="not causal"):
+        SetupDecoder(net, 2, capacity=4)
+    bnet = BeliefLike(channels=4, dim=64, heads=2, ff=64, enc_depth=1, dec_layers=2)
+    bnet.decoder.layers[1].norm_first = False
+    with pytest.raises(ValueError, match="norm_first"):
+        BeliefDecoder(bnet, torch.zeros(2, 4, 10, 10), torch.ones(2, 100, dtype=torch.bool))
+
+
 def test_weight_pack_validation_codes():
     """atx_mha_pack_weight rejects every bad argument before touching memory."""
     lib = _lib.load()

@@ -24,15 +24,18 @@ def _rel(a: torch.Tensor, b: torch.Tensor) -> float:
     return ((a.float() - b.float()).abs().max() / b.float().abs().max()).item()
 
 
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 3e-2)])
-def test_belief_decoder_matches_torch(cuda, dtype, tol):
-    """belief_net.py:159-177: causal tgt_mask, memory_key_padding_mask = ~hidden_mask."""
-    _announce(f"belief decoder {dtype}")
+@pytest.mark.parametrize("dtype,tol,b", [(torch.float32, 1e-4, 16), (torch.bfloat16, 3e-2, 16), (torch.bfloat16, 3e-2, 2048)])
+def test_belief_decoder_matches_torch(cuda, dtype, tol, b):
+    """The reference's decoder stack -- 4 layers, dim 512, 8 heads, ff 2048
+    (belief_net.py:105-114, constants.py:156-159) -- with the causal tgt_mask
+    and memory_key_padding_mask = ~hidden_mask of belief_net.py:159-177, at
+    B=16 and at config 4's B=2048, against torch's own module in fp32."""
+    _announce(f"belief decoder {dtype} b={b}")
     torch.manual_seed(0)
-    dec = belief_decoder().eval()
+    dec = belief_decoder(ff=2048, layers=4).eval()
     ref = copy.deepcopy(dec).to(cuda, dtype)
     dec = use_hip_attention(dec).to(cuda, dtype)
-    b, s = 16, 40
+    s = 40
     tgt = torch.randn(b, s, 512, device=cuda, dtype=dtype)
     mem = torch.randn(b, 100, 512, device=cuda, dtype=dtype)
     hidden = torch.rand(b, 100, device=cuda) < 0.4
@@ -81,7 +84,7 @@ def test_setup_decoder_matches_prefix_recompute(cuda, dtype, tol):
 def test_decoder_self_attention_takes_the_fused_layer(cuda, monkeypatch):
     """In inference, TransformerDecoderLayer's self-attention (self_attn(x, x, x),
     causal hint, 8 heads x 64, 40 tokens) runs as one launch of the fused
-    layer with the packed in_proj slices; it equals the projections +
+    layer from the in_proj slices (rearranged on every call); it equals the projections +
     attention kernel path to bf16 rounding and the row-major fused call
     bit for bit.  With a key padding mask it keeps the unfused path."""
     from ataraxos_amd import ops
@@ -93,7 +96,7 @@ def test_decoder_self_attention_takes_the_fused_layer(cuda, monkeypatch):
     x = torch.randn(6, 40, 512, device=cuda).bfloat16()
     calls = []
     real = ops.mha_forward
-    monkeypatch.setattr(dec_mod.ops, "mha_forward", lambda *a, **k: calls.append(k.get("packed")) or real(*a, **k))
+    monkeypatch.setattr(dec_mod.ops, "mha_forward", lambda *a, **k: calls.append(k.get("repack")) or real(*a, **k))
     with torch.no_grad():
         fused, _ = m(x, x, x, need_weights=False, is_causal=True, attn_mask=torch.zeros(40, 40, device=cuda))
         assert calls == [True]

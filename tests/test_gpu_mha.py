@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 import torch
 
-from ataraxos_amd import MultiHeadAttention, ops
+from ataraxos_amd import MultiHeadAttention, _lib, ops
 from oracle.attention import mha_forward as oracle_mha
 from tests._cases import randn, to_np64
 
@@ -268,9 +268,11 @@ def test_packed_equals_row_major(cuda, b, l, h, dtype, causal, bias):
 
 
 def test_module_repacks_after_a_weight_update(cuda):
-    """The module's cached packed weights follow in-place updates (an
-    optimizer step, load_state_dict) and replaced parameters."""
-    _announce("mha module packed-weight cache")
+    """The module's fused path rearranges the weights on every call, so it
+    follows in-place updates (an optimizer step, load_state_dict, the EMA
+    swap's ``param.data.copy_`` of ema.py:67,80, which moves no version
+    counter) and replaced parameters."""
+    _announce("mha module weight updates")
     torch.manual_seed(9)
     m = MultiHeadAttention(384, 6).to(cuda, torch.bfloat16).eval()
     x = randn((4, 100, 384), 72, torch.bfloat16).to(cuda)
@@ -292,11 +294,47 @@ def test_module_repacks_after_a_weight_update(cuda):
         y3 = m(x)
         assert torch.equal(y3, direct())
         assert not torch.equal(y3, y2)
+        # EMA apply / restore: shadow values copied in through .data
+        shadow = {n: (p.detach() * 0.75).flip(0) for n, p in m.named_parameters()}
+        versions = [p._version for p in m.parameters()]
+        for n, p in m.named_parameters():
+            p.data.copy_(shadow[n])
+        assert [p._version for p in m.parameters()] == versions  # invisible to a version check
+        y4 = m(x)
+        assert torch.equal(y4, direct())
+        assert not torch.equal(y4, y3)
+        m.fuse_layer = False
+        unfused = m(x)
+        m.fuse_layer = True
+    err = (y4.float() - unfused.float()).abs().max().item()
+    assert err <= 2e-2 * unfused.float().abs().max().item(), err
+
+
+def test_workspace_entry_point_equals_row_major(cuda):
+    """atx_mha_fwd_ws (weights rearranged into the caller's workspace on every
+    call, then the packed kernel) is bit-identical to atx_mha_fwd; a
+    workspace too small or overlapping an operand is refused."""
+    _announce("mha workspace entry point")
+    for (b, l, h, causal, bias) in [(8, 100, 6, False, False), (4, 40, 8, True, True), (3, 17, 2, False, True)]:
+        e = 64 * h
+        x = randn((b, l, e), 500 + l, torch.bfloat16).to(cuda)
+        ws, bs = layer(e, torch.bfloat16, 501 + l, bias)
+        wd = [w.to(cuda) for w in ws]
+        bd = [t.to(cuda) if t is not None else None for t in bs]
+        kw = dict(num_heads=h, b_q=bd[0], b_k=bd[1], b_v=bd[2], b_o=bd[3], causal=causal)
+        plain = ops.mha_forward(x, *wd, **kw)
+        work = torch.full((ops.mha_workspace_bytes(e) + 256,), 0xFF, dtype=torch.uint8, device=cuda)
+        got = ops.mha_forward(x, *wd, repack=True, workspace=work, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(plain, got), (b, l, h)
+    assert _lib.load().atx_mha_workspace_bytes(384) == ops.mha_workspace_bytes(384) == 4 * 384 * 384 * 2
+    with pytest.raises(ValueError, match="workspace"):
+        ops.mha_forward(x, *wd, repack=True, workspace=work[: ops.mha_workspace_bytes(e) - 1], **kw)
 
 
 def test_module_built_under_inference_mode(cuda):
-    """Parameters created under inference_mode have no version counter: the
-    module packs them on every call, so in-place changes still take effect."""
+    """Parameters created under inference_mode (no version counter): in-place
+    changes take effect on the next call."""
     _announce("mha module under inference_mode")
     x = randn((4, 100, 384), 73, torch.bfloat16).to(cuda)
     with torch.inference_mode():
