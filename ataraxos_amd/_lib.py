@@ -247,6 +247,7 @@ ENTRY_POINTS = {
     "atx_mha_pack_weight": (ctypes.c_int, [_i32, _i32, _ptr, _ptr, _ptr]),
     "atx_mha_workspace_bytes": (ctypes.c_int64, [_i32]),
     "atx_mha_fwd_ws": (ctypes.c_int, [ctypes.POINTER(MhaParams), _ptr, _i64, _ptr]),
+    "atx_mha_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(MhaParams), _ptr]),
     "atx_attn_decode_fwd": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr]),
     # include/ataraxos_rollout.h
     "atx_rollout_apply": (ctypes.c_int, [_state_ptr, _ptr, _ptr]),

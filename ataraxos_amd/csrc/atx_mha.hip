@@ -32,6 +32,8 @@
 // Rounding points match the reference's bf16 modules: Q, K, V and O are
 // rounded to the 16-bit type, every product accumulates in fp32, Y is
 // rounded once at the end.
+#include <mutex>
+
 #include "ataraxos_attn.h"
 #include "atx_common.hpp"
 
@@ -684,7 +686,7 @@ inline bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
     return x < y + nb && y < x + na;
 }
 
-// Body of atx_mha_fwd_ws: validate, check the
+// Shared body of atx_mha_fwd_ws and atx_mha_fwd_noalloc: validate, check the
 // workspace against the layer, pack the four row-major weights into it (one
 // launch), run the packed-order kernel from it.
 int mha_fwd_repack(const AtxMhaParams* p, void* ws, int64_t ws_bytes, hipStream_t st, const char* fn) {
@@ -733,6 +735,70 @@ extern "C" int64_t atx_mha_workspace_bytes(int32_t embed_dim) {
 extern "C" int atx_mha_fwd_ws(const AtxMhaParams* p, void* workspace, int64_t workspace_bytes, void* stream) {
     atx::clear_error();
     return atx::mha_fwd_repack(p, workspace, workspace_bytes, static_cast<hipStream_t>(stream), "atx_mha_fwd_ws");
+}
+
+// ---- the allocate-nothing variant -------------------------------------------
+// Device memory of atx_mha_fwd_noalloc: the four packed weights of one layer
+// (embed_dim <= 512).  Each GPU the library runs on holds its own copy until
+// the process ends.  In host code `scratch` names a host-side stand-in, not a
+// device address: only the per-device pointer from hipGetSymbolAddress is
+// ever handed to a kernel.
+static __device__ __align__(256) unsigned char scratch[ATX_MHA_NOALLOC_SCRATCH_BYTES];
+
+namespace atx {
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch`, per device
+
+// The current device's address of `scratch`, resolved once per device (with
+// that device current) on its first call.
+int scratch_for_current_device(hipStream_t st, void** out, const char* fn) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) ATX_FAIL(ATX_ERR_LAUNCH, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: device %d (at most %d devices)", fn, dev, kMaxDevices);
+    if (st) {
+        int sdev = -1;
+        e = hipStreamGetDevice(st, &sdev);
+        if (e != hipSuccess) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: hipStreamGetDevice: %s", fn, hipGetErrorString(e));
+        if (sdev != dev)
+            ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: the stream belongs to device %d, the current device is %d", fn, sdev, dev);
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            ATX_FAIL(ATX_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return ATX_OK;
+}
+}  // namespace
+}  // namespace atx
+
+extern "C" int atx_mha_fwd_noalloc(const AtxMhaParams* p, void* stream) {
+    using namespace atx;
+    const char* const fn = "atx_mha_fwd_noalloc";
+    clear_error();
+    if (!p) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: params is NULL", fn);
+    const int64_t need = atx_mha_workspace_bytes(p->embed_dim);
+    if (need > (int64_t)ATX_MHA_NOALLOC_SCRATCH_BYTES)
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: embed_dim %d needs %lld bytes of scratch, the maximum is %lld (embed_dim <= 512)",
+                 fn, p->embed_dim, (long long)need, (long long)ATX_MHA_NOALLOC_SCRATCH_BYTES);
+    {
+        // everything about the layer is checked before the first HIP call
+        MhaArgs a;
+        int np = 0;
+        size_t lds = 0;
+        if (const int rc = mha_check(p, fn, a, np, lds)) return rc;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    void* ptr = nullptr;
+    if (const int rc = scratch_for_current_device(st, &ptr, fn)) return rc;
+    return mha_fwd_repack(p, ptr, (int64_t)ATX_MHA_NOALLOC_SCRATCH_BYTES, st, fn);
 }
 
 extern "C" int atx_mha_pack_weight(int dtype, int dim, const void* w, void* packed, void* stream) {

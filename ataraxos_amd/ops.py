@@ -462,6 +462,7 @@ def mha_forward(
     packed: bool = False,
     repack: bool = False,
     workspace: torch.Tensor | None = None,
+    noalloc: bool = False,
 ) -> torch.Tensor:
     """Whole self-attention layer in one launch (no autograd):
     ``out_proj(attention(q_proj(x), k_proj(x), v_proj(x)))`` with the
@@ -478,7 +479,10 @@ def mha_forward(
       ``workspace`` (a uint8 device tensor of at least
       :func:`mha_workspace_bytes` bytes, allocated here when None) by one
       extra launch on every call, then the packed kernel (``atx_mha_fwd_ws``).
-      What the modules use: no cached copy can go stale."""
+      What the modules use: no cached copy can go stale;
+    * ``noalloc=True``: as ``repack``, with the library's own per-GPU array in
+      place of the workspace (``atx_mha_fwd_noalloc``: the C call allocates
+      nothing; embed_dim <= 512; calls that overlap on one GPU race)."""
     _require_device("mha_forward", x, w_q, w_k, w_v, w_o)
     if x.dim() != 3:
         raise ValueError("mha_forward: x must be [batch, seq, embed_dim]")
@@ -498,8 +502,8 @@ def mha_forward(
             _require_device("mha_forward", x, t)
             t = t.contiguous()
         biases.append(t)
-    if packed and repack:
-        raise ValueError("mha_forward: packed and repack are exclusive")
+    if packed + repack + noalloc > 1:
+        raise ValueError("mha_forward: packed, repack and noalloc are exclusive")
     x = _aligned_rows(x)
     ws = [_aligned_rows(w) if w.is_contiguous() else _aligned_rows(w.contiguous()) for w in (w_q, w_k, w_v, w_o)]
     if out is None:
@@ -528,6 +532,10 @@ def mha_forward(
             raise ValueError(f"mha_forward: workspace must be a contiguous uint8 tensor of >= {need} bytes on {x.device}")
         rc = _lib.load().atx_mha_fwd_ws(ctypes.byref(p), workspace.data_ptr(), workspace.numel(), _stream(x))
         _lib.check(rc, "atx_mha_fwd_ws")
+        return out
+    if noalloc:
+        with torch.cuda.device(x.device):  # the entry point uses the current device's array
+            _lib.check(_lib.call("atx_mha_fwd_noalloc", p, _stream(x)), "atx_mha_fwd_noalloc")
         return out
     name = "atx_mha_fwd_packed" if packed else "atx_mha_fwd"
     _lib.check(_lib.call(name, p, _stream(x)), name)

@@ -327,6 +327,27 @@ int64_t atx_mha_workspace_bytes(int32_t embed_dim);
  */
 int atx_mha_fwd_ws(const AtxMhaParams* params, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Size of the device array behind atx_mha_fwd_noalloc: the four packed
+ * weights at embed_dim 512 (4 * 512 * 512 * 2 bytes). */
+#define ATX_MHA_NOALLOC_SCRATCH_BYTES (2 * 1024 * 1024)
+
+/*
+ * atx_mha_fwd_ws without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The weights are rearranged into a library-owned device array of
+ * ATX_MHA_NOALLOC_SCRATCH_BYTES (one per GPU, held until the process ends),
+ * so embed_dim <= 512; a larger layer is refused with ATX_ERR_UNSUPPORTED.
+ * The call allocates nothing: its first call on a device looks up that
+ * device's array (hipGetSymbolAddress), every call launches the weight
+ * rearrangement and the layer on `stream`, which must belong to the current
+ * device.  Results are identical to atx_mha_fwd_ws and atx_mha_fwd.
+ * Every call on one GPU shares that GPU's array: calls whose executions
+ * overlap on one GPU (different streams, or graphs replayed concurrently)
+ * race on it; calls ordered on one stream do not.
+ */
+int atx_mha_fwd_noalloc(const AtxMhaParams* params, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Single-query attention over a KV cache (incremental decode)              */
 /* ------------------------------------------------------------------------ */
