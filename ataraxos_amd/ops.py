@@ -169,34 +169,66 @@ def _attention_reference_fp32(q, k, v, causal, scale, key_padding_mask):
 
 
 _BWD_DTYPES = (torch.bfloat16, torch.float16)
+_ATTN_BWD_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 _LDS_BYTES = 160 * 1024
 
 
-def _bwd_lds_bytes(head_dim: int, seq_q: int, seq_kv: int) -> int:
-    """LDS of one backward workgroup: K, V (S_kv rounded up to 32 rows), Q,
-    dO (S_q rounded up to 32 rows), and per query the log-sum-exp and delta
-    (fp32)."""
+def _bwd_lds_bytes(head_dim: int, rows_q: int, seq_kv: int, fp32: bool = False, key_chunks: int | None = None) -> int:
+    """LDS of one backward workgroup: K, V (S_kv rounded up to 32-key chunks),
+    ``rows_q`` query rows of Q and dO, and per query the log-sum-exp and
+    delta (fp32).  16-bit rows are padded to an odd number of 16-byte units
+    except at head_dim 64 / 128; fp32 rows are not padded."""
+    nkc = key_chunks if key_chunks is not None else -(-seq_kv // 32)
+    rk = nkc * 32
+    if fp32:
+        return (2 * rk + 2 * rows_q) * head_dim * 4 + rows_q * 8
     rs = head_dim * 2 if head_dim in (64, 128) else head_dim * 2 + 16
-    rk = -(-seq_kv // 32) * 32
-    rq = -(-seq_q // 32) * 32
-    return (2 * rk + 2 * rq) * rs + rq * 8
+    return (2 * rk + 2 * rows_q) * rs + rows_q * 8
+
+
+def _pow2_chunks(nkc: int) -> int:
+    return 1 if nkc <= 1 else 2 if nkc <= 2 else 4 if nkc <= 4 else 8
+
+
+def attention_backward_plan(
+    head_dim: int, seq_q: int, seq_kv: int, num_heads: int, num_kv_heads: int, dtype: torch.dtype
+) -> dict | None:
+    """How ``atx_attn_bwd`` runs this shape (the library's own rule, restated):
+    ``{"loop": bool, "key_chunks": int, "query_block": int, "lds": int}``, or
+    None when the kernels do not cover it.  ``loop`` is the variant that runs
+    the query heads of a KV group and blocks of ``query_block`` query rows one
+    after another (grouped-query attention, more than 256 queries, or more
+    query rows than LDS holds at once)."""
+    if (dtype not in _ATTN_BWD_DTYPES or num_kv_heads < 1 or num_heads % num_kv_heads
+            or head_dim % 16 or not 16 <= head_dim <= 128 or not 1 <= seq_kv <= MAX_SEQ_KV
+            or not 1 <= seq_q <= (1 << 20)):
+        return None
+    fp32 = dtype == torch.float32
+    qalign = 16 if fp32 else 32
+    rq_all = -(-seq_q // qalign) * qalign
+    exact = -(-seq_kv // 32)
+    nkc = _pow2_chunks(exact) if fp32 else exact
+    loop = num_heads != num_kv_heads or seq_q > 256 or _bwd_lds_bytes(head_dim, rq_all, seq_kv, fp32, nkc) > _LDS_BYTES
+    qb = 0
+    if loop:
+        nkc = _pow2_chunks(exact)
+        qb = min(rq_all, 256)
+        while qb > qalign and _bwd_lds_bytes(head_dim, qb, seq_kv, fp32, nkc) > _LDS_BYTES:
+            qb -= qalign
+    lds = _bwd_lds_bytes(head_dim, qb if loop else rq_all, seq_kv, fp32, nkc)
+    if lds > _LDS_BYTES:
+        return None
+    return {"loop": loop, "key_chunks": nkc, "query_block": qb, "lds": lds}
 
 
 def attention_backward_supported(
     head_dim: int, seq_q: int, seq_kv: int, num_heads: int, num_kv_heads: int, dtype: torch.dtype
 ) -> bool:
     """True when :func:`attention_backward` covers this shape and dtype:
-    bf16/fp16, no GQA, head_dim a multiple of 16 up to 128, both sequences
-    up to 256 and the workgroup's tiles within 160 KiB of LDS."""
-    return (
-        dtype in _BWD_DTYPES
-        and num_heads == num_kv_heads
-        and head_dim % 16 == 0
-        and 16 <= head_dim <= 128
-        and 1 <= seq_q <= MAX_SEQ_KV
-        and 1 <= seq_kv <= MAX_SEQ_KV
-        and _bwd_lds_bytes(head_dim, seq_q, seq_kv) <= _LDS_BYTES
-    )
+    bf16 / fp16 / fp32, GQA included, head_dim a multiple of 16 up to 128, up
+    to 256 keys and any number of queries; fp32 with head_dim >= 80 only up
+    to 128 keys (its K and V rows must fit in LDS)."""
+    return attention_backward_plan(head_dim, seq_q, seq_kv, num_heads, num_kv_heads, dtype) is not None
 
 
 def attention_backward(
@@ -211,9 +243,12 @@ def attention_backward(
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Gradients ``(dq, dk, dv)`` of :func:`attention_forward` for the
     upstream gradient ``grad_out``, given its inputs and its output ``out``
-    (all ``[B, S, H, D]``, bf16 or fp16).  One kernel launch; the softmax is
-    recomputed from Q and K, so nothing but the output is kept from the
-    forward.  Returns contiguous tensors in the inputs' dtype."""
+    (q, out, grad_out ``[B, S_q, H, D]``; k, v ``[B, S_kv, H_kv, D]``; bf16,
+    fp16 or fp32).  One kernel launch; the softmax is recomputed from Q and K,
+    so nothing but the output is kept from the forward.  With grouped-query
+    attention, dk and dv sum the gradients of the query heads that share a KV
+    head (``repeat_interleave``, attention.py:210-220).  Returns contiguous
+    tensors in the inputs' dtype, dk / dv with H_kv heads."""
     _require_device("attention_backward", q, k, v, out, grad_out)
     if not (q.dtype == k.dtype == v.dtype == out.dtype == grad_out.dtype):
         raise ValueError("attention_backward: mixed dtypes")
@@ -231,8 +266,8 @@ def attention_backward(
     if scale is None:
         scale = 1.0 / math.sqrt(d)
     dq = torch.empty((b, sq, h, d), dtype=q.dtype, device=q.device)
-    dk = torch.empty((b, skv, h, d), dtype=q.dtype, device=q.device)
-    dv = torch.empty((b, skv, h, d), dtype=q.dtype, device=q.device)
+    dk = torch.empty((b, skv, hkv, d), dtype=q.dtype, device=q.device)
+    dv = torch.empty((b, skv, hkv, d), dtype=q.dtype, device=q.device)
 
     p = _lib.AttnBwdParams()
     p.abi_version = _lib.ABI_VERSION
@@ -251,9 +286,11 @@ def attention_backward(
 
 
 class _HipAttention(torch.autograd.Function):
-    """HIP forward and, for bf16/fp16 without GQA, HIP backward
-    (:func:`attention_backward`).  fp32 inputs and GQA take their gradients
-    from an fp32 recomputation with torch ops on the same device."""
+    """HIP forward and HIP backward (:func:`attention_backward`: bf16, fp16
+    and fp32, GQA included).  The one shape family the backward kernels do
+    not hold in LDS -- fp32 with head_dim >= 80 and more than 128 keys, which
+    no network of the reference uses -- takes its gradients from an fp32
+    recomputation with torch ops on the same device."""
 
     @staticmethod
     def forward(ctx, q, k, v, causal, scale, key_padding_mask):  # type: ignore[override]

@@ -59,6 +59,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "Move-net attn fwd samples/s @B=4096,L=100 bf16; % of bf16 MFMA peak"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
+FP32_PEAK_TFLOPS = 157.3  # dense fp32 MFMA
 TRAFFIC_FILE = ROOT / "profiles" / "attn_fwd_c3_traffic.json"
 SETTLE_MS = 150.0
 
@@ -392,6 +393,18 @@ def time_backward(torch, ops, batch, dev, steps, warmup):
     leg.update({"config": "C3 layer backward, B=4096, L=100, 6x64, bf16", "kernel": "attn_bwd_16bit<bf16, D=64, NKC=4>",
                 "algorithmic_bytes_per_launch": nbytes, "tflops": flops / (ms * 1e-3) / 1e12,
                 "mfma_frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS})
+    # fp32 (what the reference's trainers run) and GQA 6/2 at the same shape
+    q32, k32, v32, do32 = (t.float() for t in (q, k, v, do))
+    o32 = ops.attention_forward(q32, k32, v32)
+    ms32 = _mean_launch_ms(torch, lambda: ops.attention_backward(q32, k32, v32, o32, do32), max(5, steps // 5), 3)
+    f = flops / (ms32 * 1e-3) / 1e12
+    leg["fp32"] = _leg("attention backward, C3 layer, fp32", ms32, 2 * nbytes, batch)
+    leg["fp32"].update({"kernel": "attn_bwd_fp32<D=64, NKC=4>", "tflops": f, "fp32_mfma_frac": f / FP32_PEAK_TFLOPS})
+    kg, vg = k[:, :, :2].contiguous(), v[:, :, :2].contiguous()
+    og = ops.attention_forward(q, kg, vg)
+    msg = _mean_launch_ms(torch, lambda: ops.attention_backward(q, kg, vg, og, do), max(5, steps // 5), 3)
+    gbytes = batch * s * d * 2 * (4 * h + 4 * 2)  # Q, O, dO, dQ per query head; K, V, dK, dV per KV head
+    leg["gqa_6_2"] = _leg("attention backward, C3 layer with 2 KV heads (GQA 6/2), bf16", msg, gbytes, batch)
     return leg
 
 

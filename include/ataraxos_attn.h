@@ -105,15 +105,15 @@ typedef struct AtxAttnParams {
 int atx_attn_fwd(const AtxAttnParams* params, void* stream);
 
 /* Gradients of atx_attn_fwd: given Q, K, V, the forward output O and dO, write
- * dQ, dK, dV (same [B, S, H, D] layouts as their tensors). */
+ * dQ ([B, S_q, H, D]), dK and dV ([B, S_kv, H_kv, D]). */
 typedef struct AtxAttnBwdParams {
     int32_t abi_version; /* must equal ATX_ABI_VERSION */
-    int32_t dtype;       /* ATX_DTYPE_BF16 or ATX_DTYPE_FP16: every tensor has this type */
+    int32_t dtype;       /* ATX_DTYPE_BF16, FP16 or FP32: every tensor has this type */
     int32_t batch;
     int32_t seq_q;
     int32_t seq_kv;
     int32_t num_heads;    /* H */
-    int32_t num_kv_heads; /* must equal H */
+    int32_t num_kv_heads; /* H_kv, divides H */
     int32_t head_dim;     /* D */
     const void* q;
     int64_t q_stride_b, q_stride_s, q_stride_h;
@@ -143,10 +143,17 @@ typedef struct AtxAttnBwdParams {
  * stratego/networks/attention.py:281-316 on the math path, or FA3 / FA2 /
  * SDPA's own backward).  The softmax is recomputed from Q and K.
  *
- * Supported range: BF16 / FP16; num_kv_heads == num_heads; head_dim a
- * multiple of 16 up to 128; 1 <= seq_q, seq_kv <= 256.  Gradients of key
- * padded or causally masked entries are zero; a query row with no usable key
- * gets dQ = 0.
+ * With G = num_heads / num_kv_heads > 1 (grouped-query attention), dK and dV
+ * of KV head j sum the gradients of query heads j*G .. j*G + G - 1, the
+ * gradient of the repeat_interleave of stratego/networks/attention.py:210-220.
+ *
+ * Supported range: BF16 / FP16 / FP32 (FP32: full fp32 products); head_dim a
+ * multiple of 16 up to 128; 1 <= seq_kv <= 256; 1 <= seq_q <= 2^20 (query
+ * rows are staged in blocks when they do not fit in LDS at once); FP32 with
+ * head_dim >= 80 only up to 128 keys.  Gradients of key padded or causally
+ * masked entries are zero; a query row with no usable key gets dQ = 0 and
+ * makes its (batch, head)'s dV NaN, as autograd through a softmax over an
+ * all -inf row does.
  */
 int atx_attn_bwd(const AtxAttnBwdParams* params, void* stream);
 

@@ -154,43 +154,50 @@ def test_attention_backward_validation_codes():
     lib = _lib.load()
     assert lib.atx_attn_bwd(None, None) == _lib.ERR_INVALID_ARGUMENT
     _expect("atx_attn_bwd", _bwd_params(abi_version=99), _lib.ERR_ABI, "abi_version")
-    _expect("atx_attn_bwd", _bwd_params(dtype=_lib.DTYPE_FP32), _lib.ERR_UNSUPPORTED, "fp32")
     _expect("atx_attn_bwd", _bwd_params(dtype=7), _lib.ERR_INVALID_ARGUMENT, "dtype")
     _expect("atx_attn_bwd", _bwd_params(seq_q=0), _lib.ERR_INVALID_ARGUMENT, "sizes")
-    _expect("atx_attn_bwd", _bwd_params(num_kv_heads=3), _lib.ERR_UNSUPPORTED, "GQA")
+    _expect("atx_attn_bwd", _bwd_params(num_kv_heads=4), _lib.ERR_INVALID_ARGUMENT, "divisible")
     _expect("atx_attn_bwd", _bwd_params(d_o=None), _lib.ERR_INVALID_ARGUMENT, "null")
     _expect("atx_attn_bwd", _bwd_params(dk=None), _lib.ERR_INVALID_ARGUMENT, "null")
     _expect("atx_attn_bwd", _bwd_params(scale=float("inf")), _lib.ERR_INVALID_ARGUMENT, "scale")
     _expect("atx_attn_bwd", _bwd_params(head_dim=24), _lib.ERR_UNSUPPORTED, "head_dim")
-    _expect("atx_attn_bwd", _bwd_params(seq_q=257), _lib.ERR_UNSUPPORTED, "256")
+    _expect("atx_attn_bwd", _bwd_params(seq_kv=257), _lib.ERR_UNSUPPORTED, "256")
     _expect("atx_attn_bwd", _bwd_params(do_stride_s=385), _lib.ERR_INVALID_ARGUMENT, "16-byte")
     _expect("atx_attn_bwd", _bwd_params(dq=(1 << 20) + 8), _lib.ERR_INVALID_ARGUMENT, "16-byte")
     _expect("atx_attn_bwd", _bwd_params(v_stride_s=-384), _lib.ERR_UNSUPPORTED, ">= 0")
     _expect("atx_attn_bwd", _bwd_params(dv_stride_s=32), _lib.ERR_INVALID_ARGUMENT, "overlap")
-    _expect("atx_attn_bwd", _bwd_params(head_dim=128, seq_q=256, seq_kv=256, **{
+    _expect("atx_attn_bwd", _bwd_params(dtype=_lib.DTYPE_FP32, head_dim=128, seq_q=256, seq_kv=256, **{
         f"{n}_stride_s": 768 for n in ("q", "k", "v", "o", "do", "dq", "dk", "dv")}), _lib.ERR_UNSUPPORTED, "LDS")
 
 
 def test_backward_lds_rule_matches_python_predicate():
-    """The library's LDS bound and ``ops.attention_backward_supported`` agree:
-    every shape the predicate refuses for LDS alone is refused by the library
-    with the same byte count.  Shapes that pass are not called here, since
-    their pointers are fake."""
+    """The library's LDS rule and ``ops.attention_backward_plan`` agree: every
+    shape the plan refuses is refused by the library with the same byte
+    count.  Shapes that pass are not called here, since their pointers are
+    fake.  16-bit shapes all pass (queries are staged in blocks when needed);
+    fp32 refuses head_dim >= 80 beyond 128 keys."""
     from ataraxos_amd import ops
 
     refused = 0
-    for d in (16, 32, 48, 64, 80, 96, 112, 128):
-        for sq, skv in ((100, 100), (256, 256), (40, 100), (256, 1), (1, 256), (200, 200), (129, 256)):
-            if ops.attention_backward_supported(d, sq, skv, 4, 4, torch.bfloat16):
-                continue
-            strides = {f"{n}_stride_s": 2 * d for n in ("q", "k", "v", "o", "do", "dq", "dk", "dv")}
-            p = _bwd_params(head_dim=d, seq_q=sq, seq_kv=skv, num_heads=1, num_kv_heads=1, **strides)
-            assert _lib.call("atx_attn_bwd", p, None) == _lib.ERR_UNSUPPORTED
-            assert f"need {ops._bwd_lds_bytes(d, sq, skv)} bytes of LDS" in _lib.last_error(), (d, sq, skv)
-            refused += 1
-    assert refused >= 5
-    assert ops.attention_backward_supported(64, 256, 256, 6, 6, torch.bfloat16)
-    assert ops.attention_backward_supported(64, 100, 100, 6, 6, torch.bfloat16)
+    for dtype, code in ((torch.bfloat16, _lib.DTYPE_BF16), (torch.float32, _lib.DTYPE_FP32)):
+        for d in (16, 32, 48, 64, 80, 96, 112, 128):
+            for sq, skv in ((100, 100), (256, 256), (40, 100), (256, 1), (1, 256), (200, 200), (129, 256), (600, 160)):
+                plan = ops.attention_backward_plan(d, sq, skv, 4, 4, dtype)
+                if plan is not None:
+                    continue
+                assert dtype == torch.float32 and d >= 80 and skv > 128, (d, sq, skv)
+                strides = {f"{n}_stride_s": 2 * d for n in ("q", "k", "v", "o", "do", "dq", "dk", "dv")}
+                p = _bwd_params(dtype=code, head_dim=d, seq_q=sq, seq_kv=skv, num_heads=1, num_kv_heads=1, **strides)
+                assert _lib.call("atx_attn_bwd", p, None) == _lib.ERR_UNSUPPORTED
+                want = ops._bwd_lds_bytes(d, 16, skv, True, 8)
+                assert f"need {want} bytes of LDS" in _lib.last_error(), (d, sq, skv, _lib.last_error())
+                refused += 1
+    assert refused >= 8
+    for args in ((64, 256, 256, 6, 6), (64, 100, 100, 6, 6), (128, 256, 256, 8, 2), (48, 101, 101, 8, 8)):
+        assert ops.attention_backward_supported(*args, torch.bfloat16)
+    assert ops.attention_backward_plan(64, 100, 100, 6, 6, torch.bfloat16) == {
+        "loop": False, "key_chunks": 4, "query_block": 0, "lds": 66560}
+    assert ops.attention_backward_plan(64, 100, 100, 8, 2, torch.bfloat16)["loop"]
 
 
 def test_policy_validation_codes():
