@@ -15,34 +15,15 @@
 // ([RP x RP], zero-padded to a multiple of 32); Q and K rows are staged next
 // to it.  Phase 2 runs dq^T = K^T dL^T and dk^T = Q^T dL as 16x16x32 MFMA
 // tiles, one 16-row output tile per wave pass, with K^T, Q^T and dL (for dk)
-// fed by transposing LDS reads.  Every output has one owner and every sum a
+// fed by transposing LDS reads.  Rows wider than 128 (the reference's
+// policy_d_model = 384, move_net.py:151) are processed in 64-column slices,
+// dL staying resident: columns c of dq and dk depend only on columns c of k
+// and q.  Every output has one owner and every sum a
 // fixed order: the result does not depend on timing.
-#include "ataraxos_attn.h"
-#include "atx_common.hpp"
+#include "atx_kq_bwd.hpp"
 
 namespace atx {
 
-struct KqBwdArgs {
-    const void* q;
-    const void* k;
-    int64_t qsb, ksb;
-    int qss, kss;  // row strides (elements)
-    const uint8_t* mask;
-    int64_t msb;
-    int mss;
-    const float* grad;
-    int64_t gsb;
-    const float* probs;
-    int64_t psb;
-    void* dq;
-    void* dk;
-    int64_t dqsb, dksb;
-    int dqss, dkss;
-    int S;
-    float scale;
-    int mask_al4;   // mask base and strides are multiples of 4 bytes
-    int grad_vec;   // S % 4 == 0 and every G / P row starts 16-byte aligned
-};
 
 namespace {
 
@@ -83,7 +64,8 @@ inline size_t kq_bwd_lds_bytes(int D, int nkc) {
     return (size_t)rp * rs_g + (size_t)2 * rp * rs + kWaves * 4;
 }
 
-// NKC = 32-square chunks (S <= 32 * NKC); PROBS: G is the gradient of P.
+// NKC = 32-square chunks (S <= 32 * NKC); PROBS: G is the gradient of P;
+// D = the column slice width (a.nd slices of it make a row).
 template <typename T, int D, int NKC, bool PROBS>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kq_bwd_occ<D, NKC>(), 8)))
 void kq_bwd_16bit(KqBwdArgs a) {
@@ -108,113 +90,13 @@ void kq_bwd_16bit(KqBwdArgs a) {
     const int b = blockIdx.x;
     const int S = a.S;
 
-    const rsrc_t rg = make_rsrc(a.grad + b * a.gsb, (uint32_t)(S * S * 4));
-    const rsrc_t rp = make_rsrc(PROBS ? a.probs + b * a.psb : a.grad, PROBS ? (uint32_t)(S * S * 4) : 0u);
-    const uint8_t* const mrow0 = a.mask ? a.mask + b * a.msb : nullptr;
-    const rsrc_t rm = make_rsrc(mrow0 ? mrow0 : a.mask, mrow0 ? (uint32_t)((S - 1) * a.mss + S) : 0u);
-
-    // ---- phase 1: dL into LDS -------------------------------------------------
-    // Thread t handles dL chunks t, t + 512, ...: row i = idx / GC, columns
-    // j = 8 * (idx % GC) .. + 7.
-    float gv[PERT][8], pv[PROBS ? PERT : 1][8];
-    uint32_t legal[PERT];  // bit e: entry j0 + e is legal and inside the sample
-    float part = 0.f;
-#pragma unroll
-    for (int u = 0; u < PERT; ++u) {
-        const int idx = tid + u * kThreads;
-        const int i = idx / GC, j0 = (idx - (idx / GC) * GC) * 8;
-        const bool live = idx < RP * GC && i < S && j0 < S;
-        // G (and P) values
-        if (a.grad_vec) {
-            const uint32_t off = live ? (uint32_t)(i * S + j0) * 4 : kOut;
-            // j0 + 4 < S or the second half starts the next row: not loaded
-            const uint32_t off2 = live && j0 + 4 < S ? off + 16 : kOut;
-            const f32x4 g0 = as_f32x4(buf_ld16(rg, off)), g1 = as_f32x4(buf_ld16(rg, off2));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) gv[u][e] = g0[e], gv[u][4 + e] = g1[e];
-            if constexpr (PROBS) {
-                const f32x4 p0 = as_f32x4(buf_ld16(rp, off)), p1 = as_f32x4(buf_ld16(rp, off2));
-#pragma unroll
-                for (int e = 0; e < 4; ++e) pv[u][e] = p0[e], pv[u][4 + e] = p1[e];
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t off = live && j0 + e < S ? (uint32_t)(i * S + j0 + e) * 4 : kOut;
-                gv[u][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, (int)off, 0, 0));
-                if constexpr (PROBS)
-                    pv[u][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, (int)off, 0, 0));
-            }
-        }
-        // legality bits
-        uint32_t lb = 0;
-        if (live) {
-            const int nin = min(S - j0, 8);
-            const uint32_t in_bits = (1u << nin) - 1u;
-            if (!mrow0) {
-                lb = in_bits;
-            } else if (a.mask_al4) {
-                const uint32_t moff = (uint32_t)(i * a.mss + j0);
-                uint32_t w[2];
-#pragma unroll
-                for (int d = 0; d < 2; ++d) {
-                    if (j0 + 4 * d + 4 <= S) {
-                        w[d] = __builtin_amdgcn_raw_buffer_load_b32(rm, (int)(moff + 4 * d), 0, 0);
-                    } else {
-                        w[d] = 0;
-                        for (int e = 0; j0 + 4 * d + e < S; ++e)
-                            w[d] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rm, (int)(moff + 4 * d + e), 0, 0) << (8 * e);
-                    }
-                }
-#pragma unroll
-                for (int e = 0; e < 8; ++e) lb |= (((w[e >> 2] >> (8 * (e & 3))) & 0xffu) != 0 ? 1u : 0u) << e;
-                lb &= in_bits;
-            } else {
-                for (int e = 0; e < nin; ++e)
-                    lb |= (__builtin_amdgcn_raw_buffer_load_b8(rm, (int)(i * a.mss + j0 + e), 0, 0) != 0 ? 1u : 0u) << e;
-            }
-        }
-        legal[u] = lb;
-        if constexpr (PROBS) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) part = __builtin_fmaf(gv[u][e], pv[u][e], part);
-        }
-    }
-    float sigma = 0.f;
-    if constexpr (PROBS) {
-        // sum(G * P) over the sample: per wave, then the 8 wave sums in order
-#pragma unroll
-        for (int x = 32; x >= 1; x >>= 1) part += shfl_xor(part, x);
-        if (lane == 0) lds_st4(sred + wave * 4, __builtin_bit_cast(uint32_t, part));
-        __syncthreads();
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) sigma += __builtin_bit_cast(float, lds_ld4(sred + w * 4));
-    }
-#pragma unroll
-    for (int u = 0; u < PERT; ++u) {
-        const int idx = tid + u * kThreads;
-        if (idx >= RP * GC) break;
-        const int i = idx / GC, c = idx - (idx / GC) * GC;
-        float dl[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float x = PROBS ? pv[u][e] * (gv[u][e] - sigma) : gv[u][e];
-            dl[e] = ((legal[u] >> e) & 1u) ? x : 0.f;
-        }
-        lds_st16(sg + chunk_off_w<RP>(i, c), u32x4{M::pack2(dl[0], dl[1]), M::pack2(dl[2], dl[3]),
-                                                      M::pack2(dl[4], dl[5]), M::pack2(dl[6], dl[7])});
-    }
-    // ---- Q and K rows (rows past S read 0) -------------------------------------
-    {
-        const rsrc_t rq = make_rsrc(static_cast<const T*>(a.q) + b * a.qsb, (uint32_t)(((S - 1) * a.qss + D) * 2));
-        const rsrc_t rk = make_rsrc(static_cast<const T*>(a.k) + b * a.ksb, (uint32_t)(((S - 1) * a.kss + D) * 2));
-        for (int idx = tid; idx < RP * CH; idx += kThreads) {
-            const int r = idx / CH, c = idx - (idx / CH) * CH;
-            lds_st16(sq + chunk_off_w<D>(r, c), buf_ld16(rq, (uint32_t)(r * a.qss + c * 8) * 2));
-            lds_st16(sk + chunk_off_w<D>(r, c), buf_ld16(rk, (uint32_t)(r * a.kss + c * 8) * 2));
-        }
-    }
-    __syncthreads();
+    lds_t* const sg_ = sg;
+    kq_bwd_dl<RP, PROBS>(a, b, sred, [&](int i, int c, const float (&dl)[8]) {
+        lds_st16(sg_ + chunk_off_w<RP>(i, c), u32x4{M::pack2(dl[0], dl[1]), M::pack2(dl[2], dl[3]),
+                                                       M::pack2(dl[4], dl[5]), M::pack2(dl[6], dl[7])});
+    });
+    const rsrc_t rq = make_rsrc(static_cast<const T*>(a.q) + b * a.qsb, (uint32_t)(((S - 1) * a.qss + a.Dfull) * 2));
+    const rsrc_t rk = make_rsrc(static_cast<const T*>(a.k) + b * a.ksb, (uint32_t)(((S - 1) * a.kss + a.Dfull) * 2));
 
     // ---- phase 2: dq^T = K^T dL^T, dk^T = Q^T dL --------------------------------
     // Transposing reads of Q / K: input lane a4 + 4t of a 16-lane group points
@@ -225,11 +107,12 @@ void kq_bwd_16bit(KqBwdArgs a) {
     for (int dt = 0; dt < NDT; ++dt) troff[dt] = quad_off_w<D>(4 * g + (m >> 2), (m & 3) * QD + 4 * dt);
     const T* const dqbase = static_cast<const T*>(a.dq) + b * a.dqsb;
     const T* const dkbase = static_cast<const T*>(a.dk) + b * a.dksb;
-    const rsrc_t rdq = make_rsrc(dqbase, (uint32_t)(((S - 1) * a.dqss + D) * 2));
-    const rsrc_t rdk = make_rsrc(dkbase, (uint32_t)(((S - 1) * a.dkss + D) * 2));
+    const rsrc_t rdq = make_rsrc(dqbase, (uint32_t)(((S - 1) * a.dqss + a.Dfull) * 2));
+    const rsrc_t rdk = make_rsrc(dkbase, (uint32_t)(((S - 1) * a.dkss + a.Dfull) * 2));
+    int col0 = 0;  // first column of the current slice
     auto store_row = [&](rsrc_t r, int ss, int row, const f32x4 (&x)[NDT]) {
         const float mul = a.scale;
-        const uint32_t base = (uint32_t)(row * ss + g * QD) * 2;
+        const uint32_t base = (uint32_t)(row * ss + col0 + g * QD) * 2;
         if constexpr (QD % 8 == 0) {
 #pragma unroll
             for (int dt = 0; dt < NDT; dt += 2)
@@ -245,6 +128,16 @@ void kq_bwd_16bit(KqBwdArgs a) {
         }
     };
     const int ntile = (S + 15) >> 4;
+    for (int dc = 0; dc < a.nd; ++dc) {
+    col0 = dc * D;
+    if (dc > 0) __syncthreads();  // every wave is done with the previous slice
+    // ---- Q and K rows of the slice (rows past S read 0) -------------------------
+    for (int idx = tid; idx < RP * CH; idx += kThreads) {
+        const int r = idx / CH, c = idx - (idx / CH) * CH;
+        lds_st16(sq + chunk_off_w<D>(r, c), buf_ld16(rq, (uint32_t)(r * a.qss + col0 + c * 8) * 2));
+        lds_st16(sk + chunk_off_w<D>(r, c), buf_ld16(rk, (uint32_t)(r * a.kss + col0 + c * 8) * 2));
+    }
+    __syncthreads();
     for (int t = wave; t < 2 * ntile; t += kWaves) {
         f32x4 acc[NDT];
 #pragma unroll
@@ -283,6 +176,7 @@ void kq_bwd_16bit(KqBwdArgs a) {
             }
             store_row(rdk, a.dkss, jt * 16 + m, acc);
         }
+    }
     }
 }
 
@@ -334,10 +228,10 @@ extern "C" int atx_kq_bwd(const AtxKqBwdParams* p, void* stream) {
     if (!p) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_kq_bwd: params is NULL");
     if (p->abi_version != ATX_ABI_VERSION)
         ATX_FAIL(ATX_ERR_ABI, "atx_kq_bwd: abi_version %d, library is %d", p->abi_version, ATX_ABI_VERSION);
-    if (p->dtype != ATX_DTYPE_BF16 && p->dtype != ATX_DTYPE_FP16) {
-        if (p->dtype == ATX_DTYPE_FP32) ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_bwd: fp32 is not supported");
+    if (p->dtype != ATX_DTYPE_BF16 && p->dtype != ATX_DTYPE_FP16 && p->dtype != ATX_DTYPE_FP32)
         ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_kq_bwd: unknown dtype %d", p->dtype);
-    }
+    const bool f32 = p->dtype == ATX_DTYPE_FP32;
+    const int es = f32 ? 4 : 2;
     if (p->batch < 1 || p->seq < 1 || p->dim < 1)
         ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_kq_bwd: sizes must be >= 1 (batch %d, seq %d, dim %d)", p->batch, p->seq,
                  p->dim);
@@ -349,11 +243,12 @@ extern "C" int atx_kq_bwd(const AtxKqBwdParams* p, void* stream) {
     if (!(p->scale > 0.f) || p->scale == __builtin_inff())
         ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_kq_bwd: scale must be finite and > 0 (got %g)", (double)p->scale);
     if (p->seq > 128) ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_bwd: seq %d not supported (<= 128)", p->seq);
-    if (p->dim % 16 != 0 || p->dim > 128)
-        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_bwd: dim %d not supported (multiple of 16, <= 128)", p->dim);
+    if (p->dim % 16 != 0 || (!f32 && p->dim > 128 && p->dim % 64 != 0) || p->dim > 4096)
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_bwd: dim %d not supported (multiple of 16 up to 128, of 64 up to 4096%s)",
+                 p->dim, f32 ? "" : "; fp32: of 16 up to 4096");
     const int D = p->dim, S = p->seq;
-    auto rows16 = [](const void* base, int64_t sb, int64_t ss) {
-        return aligned16(base) && ((sb * 2) & 15) == 0 && ((ss * 2) & 15) == 0;
+    auto rows16 = [&](const void* base, int64_t sb, int64_t ss) {
+        return aligned16(base) && ((sb * es) & 15) == 0 && ((ss * es) & 15) == 0;
     };
     // Row strides of a one-row sample are never used.
     auto sstride = [&](int64_t s) { return S == 1 ? (int64_t)D : s; };
@@ -363,7 +258,7 @@ extern "C" int atx_kq_bwd(const AtxKqBwdParams* p, void* stream) {
         !rows16(p->dk, p->dk_stride_b, dkss))
         ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_kq_bwd: every q/k/dq/dk row must start on a 16-byte boundary");
     for (int64_t s : {qss, kss, dqss, dkss})
-        if (s < 0 || (int64_t)(S + 32) * s * 2 + D * 2 > 0x7fffffffLL)
+        if (s < 0 || (int64_t)(S + 32) * s * es + D * es > 0x7fffffffLL)
             ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_bwd: row strides must be >= 0 and one sample < 2 GiB");
     if (dqss < D || dkss < D) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "atx_kq_bwd: dq/dk rows overlap");
     if (((uintptr_t)p->grad & 3) != 0 || p->grad_stride_b < (int64_t)S * S ||
@@ -386,18 +281,24 @@ extern "C" int atx_kq_bwd(const AtxKqBwdParams* p, void* stream) {
     a.dqsb = p->dq_stride_b; a.dksb = p->dk_stride_b;
     a.dqss = (int)dqss; a.dkss = (int)dkss;
     a.S = S;
+    a.Dfull = D;
+    // 16-bit: rows up to 128 wide in one slice, wider ones in 64-column
+    // slices; fp32: slices of 32 or 16 columns
+    const int dslice = f32 ? (D % 32 == 0 ? 32 : 16) : (D <= 128 ? D : 64);
+    a.nd = D / dslice;
     a.scale = p->scale;
     a.mask_al4 = p->mask && ((uintptr_t)p->mask & 3) == 0 && (p->mask_stride_b & 3) == 0 && (p->mask_stride_s & 3) == 0;
     a.grad_vec = S % 4 == 0 && aligned16(p->grad) && (p->grad_stride_b & 3) == 0 &&
                  (!probs || (aligned16(p->probs) && (p->probs_stride_b & 3) == 0));
     const int nkc = S <= 64 ? 2 : (S + 31) / 32;
-    const size_t lds = kq_bwd_lds_bytes(D, nkc);
+    const size_t lds = f32 ? kq_bwd_fp32_lds_bytes(dslice, nkc) : kq_bwd_lds_bytes(dslice, nkc);
     if (lds > 160 * 1024)
         ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_bwd: seq %d, dim %d need %zu bytes of LDS (> 160 KiB)", S, D, lds);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (f32) return dispatch_kq_bwd_fp32(probs, dslice, nkc, p->batch, lds, st, a);
     if (p->dtype == ATX_DTYPE_BF16)
-        return probs ? dispatch_kq_bwd<__bf16, true>(D, nkc, p->batch, lds, st, a)
-                     : dispatch_kq_bwd<__bf16, false>(D, nkc, p->batch, lds, st, a);
-    return probs ? dispatch_kq_bwd<_Float16, true>(D, nkc, p->batch, lds, st, a)
-                 : dispatch_kq_bwd<_Float16, false>(D, nkc, p->batch, lds, st, a);
+        return probs ? dispatch_kq_bwd<__bf16, true>(dslice, nkc, p->batch, lds, st, a)
+                     : dispatch_kq_bwd<__bf16, false>(dslice, nkc, p->batch, lds, st, a);
+    return probs ? dispatch_kq_bwd<_Float16, true>(dslice, nkc, p->batch, lds, st, a)
+                 : dispatch_kq_bwd<_Float16, false>(dslice, nkc, p->batch, lds, st, a);
 }

@@ -389,8 +389,11 @@ def kq_policy(
 
 def kq_policy_backward_supported(seq: int, dim: int, dtype: torch.dtype) -> bool:
     """True when :func:`kq_policy_backward` covers this shape and dtype:
-    bf16/fp16, ``seq`` up to 128, ``dim`` a multiple of 16 up to 128."""
-    return dtype in _BWD_DTYPES and 1 <= seq <= 128 and dim % 16 == 0 and 16 <= dim <= 128
+    bf16 / fp16 / fp32, ``seq`` up to 128, ``dim`` a multiple of 16 up to 128
+    or of 64 up to 4096 (the reference's policy head has dim 384); fp32: any
+    multiple of 16 up to 4096."""
+    return (dtype in _ATTN_BWD_DTYPES and 1 <= seq <= 128 and dim % 16 == 0 and 16 <= dim <= 4096
+            and (dim <= 128 or dim % 64 == 0 or dtype == torch.float32))
 
 
 def kq_policy_backward(

@@ -12,7 +12,8 @@ caller applies to those logits (``stratego/training/selfplay.py:284``,
 
 Gradients (the Move trainer's ``loss.backward()``, move_trainer.py:140) of
 either output go through one HIP launch (:func:`ops.kq_policy_backward`) for
-bf16/fp16 q, k; fp32 inputs are differentiated with torch ops in fp32.
+bf16, fp16 and fp32 q, k, at the reference's d = 384 too; only a 16-bit d
+above 128 that is not a multiple of 64 is differentiated with torch ops.
 """
 
 from __future__ import annotations

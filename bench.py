@@ -427,6 +427,19 @@ def time_kq_backward(torch, ops, batch, dev, steps, warmup):
         # G (and P) fp32 + legality bytes + q, k read; dq, dk written
         nbytes = batch * (s * s * 4 * (2 if output == "probs" else 1) + s * s + 4 * s * d * 2)
         legs[output] = _leg(f"policy head backward, gradient of the {output}", ms, nbytes, batch)
+    # fp32 q/k at C2, and the reference Move network's own head: 101 squares, d=384
+    q32, k32 = q.float(), k.float()
+    ms = _mean_launch_ms(torch, lambda: ops.kq_policy_backward(q32, k32, grad, mask), max(5, steps // 5), 3)
+    legs["logits_fp32"] = _leg("policy head backward, gradient of the logits, fp32 q/k", ms,
+                               batch * (s * s * 4 + s * s + 4 * s * d * 4), batch)
+    s2, d2 = 101, 384
+    q2 = torch.randn(batch, s2, d2, generator=g, device=dev).to(torch.bfloat16)
+    k2 = torch.randn(batch, s2, d2, generator=g, device=dev).to(torch.bfloat16)
+    m2 = torch.rand(batch, s2, s2, generator=g, device=dev) < 0.02
+    g2 = torch.randn(batch, s2 * s2, generator=g, device=dev)
+    ms = _mean_launch_ms(torch, lambda: ops.kq_policy_backward(q2, k2, g2, m2), max(5, steps // 5), 3)
+    legs["logits_move_ref_d384"] = _leg("policy head backward at the reference Move head's shape (101 squares, d=384), bf16",
+                                        ms, batch * (s2 * s2 * 4 + s2 * s2 + 4 * s2 * d2 * 2), batch)
     return {"config": "C2 policy head backward, B=4096, 100x100, d=64, bf16 q/k, fp32 gradient", "legs": legs}
 
 

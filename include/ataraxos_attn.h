@@ -213,14 +213,17 @@ int atx_kq_masked_softmax_fwd(const AtxKqParams* params, void* stream);
  * then dq[b] = scale * dL k[b] and dk[b] = scale * dL^T q[b] (dL as
  * [seq, seq]), written in q's dtype.  Masked entries get no gradient, as
  * through masked_fill; a sample with no legal entry gets dq = dk = 0.
- * 16-bit q / k only (ATX_DTYPE_BF16 or FP16), dim a multiple of 16 up to 128.
+ * q / k in BF16, FP16 or FP32 (FP32: fp32 products, the precision the
+ * reference trains in).  dim a multiple of 16 up to 128, or of 64 up to 4096
+ * (the reference's policy_d_model = 384, stratego/networks/move_net.py:151);
+ * FP32: a multiple of 16 up to 4096.
  */
 typedef struct AtxKqBwdParams {
     int32_t abi_version;
-    int32_t dtype;    /* of q, k, dq, dk: ATX_DTYPE_BF16 or FP16 */
+    int32_t dtype;    /* of q, k, dq, dk: ATX_DTYPE_BF16, FP16 or FP32 */
     int32_t batch;
     int32_t seq;      /* 1..128 */
-    int32_t dim;      /* multiple of 16, <= 128 */
+    int32_t dim;      /* see above */
     int32_t out_mode; /* ATX_KQ_OUT_*: what `grad` is the gradient of */
     const void* q;
     int64_t q_stride_b, q_stride_s;

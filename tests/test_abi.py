@@ -233,11 +233,13 @@ def test_policy_backward_validation_codes():
     assert _lib.load().atx_kq_bwd(None, None) == _lib.ERR_INVALID_ARGUMENT
     for field, value, code, text in [
         ("abi_version", 3, _lib.ERR_ABI, "abi_version"),
-        ("dtype", _lib.DTYPE_FP32, _lib.ERR_UNSUPPORTED, "fp32"),
+        ("dtype", 9, _lib.ERR_INVALID_ARGUMENT, "dtype"),
         ("out_mode", 5, _lib.ERR_INVALID_ARGUMENT, "out_mode"),
         ("out_mode", _lib.KQ_OUT_PROBS, _lib.ERR_INVALID_ARGUMENT, "null"),  # probs mode needs probs
         ("seq", 129, _lib.ERR_UNSUPPORTED, "seq"),
         ("dim", 40, _lib.ERR_UNSUPPORTED, "dim"),
+        ("dim", 144, _lib.ERR_UNSUPPORTED, "dim"),   # > 128: a multiple of 64
+        ("dim", 4160, _lib.ERR_UNSUPPORTED, "dim"),
         ("scale", 0.0, _lib.ERR_INVALID_ARGUMENT, "scale"),
         ("grad_stride_b", 9999, _lib.ERR_INVALID_ARGUMENT, "stride"),
         ("dq_stride_s", 32, _lib.ERR_INVALID_ARGUMENT, "overlap"),

@@ -36,16 +36,22 @@ def _announce(msg: str) -> None:
     sys.stdout.flush()
 
 
+# fp32 q, k (fp32 products): 1e-4 of the gradient's scale, 2e-5 Frobenius
+FP32_REL_MAX = 1e-4
+FP32_REL_FRO = 2e-5
+
+
 def assert_grad_close(got: torch.Tensor, ref: np.ndarray, what: str) -> None:
+    rel_max, rel_fro = (FP32_REL_MAX, FP32_REL_FRO) if got.dtype == torch.float32 else (REL_MAX, REL_FRO)
     g = to_np64(got)
     assert g.shape == ref.shape, f"{what}: shape {g.shape} vs {ref.shape}"
     assert np.isfinite(g).all(), f"{what}: non-finite values"
     scale = max(float(np.max(np.abs(ref))), ZERO_FLOOR)
     err = float(np.max(np.abs(g - ref)))
-    assert err <= REL_MAX * scale, f"{what}: max-abs {err:.3e} > {REL_MAX} * {scale:.3e}"
+    assert err <= rel_max * scale, f"{what}: max-abs {err:.3e} > {rel_max} * {scale:.3e}"
     if scale > ZERO_FLOOR:
         fro = float(np.linalg.norm(g - ref) / np.linalg.norm(ref))
-        assert fro <= REL_FRO, f"{what}: relative Frobenius error {fro:.3e} > {REL_FRO}"
+        assert fro <= rel_fro, f"{what}: relative Frobenius error {fro:.3e} > {rel_fro}"
 
 
 def run_case(cuda, b, s, d, dtype, output, p_legal=0.02, seed=0, scale=None, empty_sample=False, mask_view=False):
@@ -174,13 +180,100 @@ def test_policy_head_module_gradients(cuda):
     assert err <= REL_MAX * want.abs().max().item(), err
 
 
-def test_fp32_and_unsupported_dims_fall_back(cuda):
-    q = torch.randn(4, 100, 64, device=cuda)
-    with pytest.raises(NotImplementedError):
-        ops.kq_policy_backward(q, q, torch.zeros(4, 10000, device=cuda))
-    qb = torch.randn(4, 100, 40, device=cuda, dtype=torch.bfloat16)
+@pytest.mark.parametrize("d", [192, 384, 512])
+@pytest.mark.parametrize("output", ["logits", "probs"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_wide_dims(cuda, d, output, dtype):
+    """policy_d_model wider than 128, in 64-column slices: the reference's
+    Move network builds KeyQueryPolicyHead(dim, dim) with dim 384
+    (move_net.py:151, constants.py:149)."""
+    assert ops.kq_policy_backward_supported(101, d, dtype)
+    run_case(cuda, 6, 101, d, dtype, output, p_legal=0.05, seed=300 + d)
+
+
+def test_reference_move_policy_head_gradients(cuda, monkeypatch):
+    """KeyQueryPolicyHead(384, 384) at the Move network's 101 tokens, bf16:
+    the gradients run through atx_kq_bwd (no torch fallback) and the input
+    gradient agrees with float64 autograd of the head's math."""
+    _announce("kq bwd reference move head 384")
+    import ataraxos_amd.policy as pol
+
+    calls = []
+    real = ops.kq_policy_backward
+    monkeypatch.setattr(pol.ops, "kq_policy_backward", lambda *a, **k: calls.append(a[0].shape) or real(*a, **k))
+    monkeypatch.setattr(pol, "_logit_grads", lambda *a, **k: pytest.fail("torch fallback taken"))
+    torch.manual_seed(4)
+    head = KeyQueryPolicyHead(384, 384).to(cuda, torch.bfloat16)
+    x = randn((4, 101, 384), 90, torch.bfloat16).to(cuda).requires_grad_(True)
+    mask = legal_mask(4, 101, 91, 0.05).to(cuda)
+    g = randn((4, 101 * 101), 92, torch.float32).to(cuda)
+    out = head(x, mask)
+    (gx,) = torch.autograd.grad(out.float(), (x,), g)
+    assert calls == [torch.Size([4, 101, 384])]
+    h64 = KeyQueryPolicyHead(384, 384).double()
+    h64.load_state_dict({n: t.double().cpu() for n, t in head.state_dict().items()})
+    x64 = x.detach().double().cpu().requires_grad_(True)
+    (want,) = torch.autograd.grad(h64(x64, mask.cpu()), (x64,), g.double().cpu())
+    err = (gx.double().cpu() - want).abs().max().item()
+    assert err <= REL_MAX * want.abs().max().item(), err
+
+
+@pytest.mark.parametrize("output", ["logits", "probs"])
+@pytest.mark.parametrize("s,d", [(100, 64), (101, 384), (33, 16), (64, 48), (128, 128), (100, 400), (17, 96)])
+def test_fp32(cuda, s, d, output):
+    """fp32 q, k -- the precision the reference's Move trainer runs its policy
+    head in -- through the fp32 kernel (fp32 products)."""
+    assert ops.kq_policy_backward_supported(s, d, torch.float32)
+    run_case(cuda, 4, s, d, torch.float32, output, p_legal=0.05, seed=400 + s + d)
+
+
+def test_config2_fp32_full_batch(cuda):
+    """C2's shape (B=4096, 100 x 100, d=64) in fp32: sampled rows against the
+    oracle, and a sub-batch gives bit-identical rows."""
+    b, s, d = 4096, 100, 64
+    _announce("kq bwd C2 fp32 full batch")
+    q, k = randn((b, s, d), 410, torch.float32), randn((b, s, d), 411, torch.float32)
+    mask = legal_mask(b, s, 412, 0.02)
+    grad = randn((b, s * s), 413, torch.float32)
+    qd, kd, md, gd = q.to(cuda), k.to(cuda), mask.to(cuda), grad.to(cuda)
+    dq, dk = ops.kq_policy_backward(qd, kd, gd, md, 0.125)
+    idx = torch.tensor([0, 1, 2047, 4095, 1234, 3000])
+    ref = kq_backward(to_np64(q[idx]), to_np64(k[idx]), mask[idx].numpy(), 0.125, grad[idx].double().numpy())
+    assert_grad_close(dq[idx.to(cuda)], ref[0], "C2 fp32 dq")
+    assert_grad_close(dk[idx.to(cuda)], ref[1], "C2 fp32 dk")
+    sdq, sdk = ops.kq_policy_backward(qd[100:200], kd[100:200], gd[100:200], md[100:200], 0.125)
+    torch.cuda.synchronize()
+    assert torch.equal(sdq, dq[100:200]) and torch.equal(sdk, dk[100:200])
+
+
+def test_fp32_reference_move_policy_head(cuda, monkeypatch):
+    """KeyQueryPolicyHead(384, 384) in fp32 at 101 tokens: its gradients run
+    through atx_kq_bwd, and the input gradient matches float64 autograd."""
+    _announce("kq bwd reference move head 384 fp32")
+    import ataraxos_amd.policy as pol
+
+    monkeypatch.setattr(pol, "_logit_grads", lambda *a, **k: pytest.fail("torch fallback taken"))
+    torch.manual_seed(5)
+    head = KeyQueryPolicyHead(384, 384).to(cuda)
+    x = randn((4, 101, 384), 93, torch.float32).to(cuda).requires_grad_(True)
+    mask = legal_mask(4, 101, 94, 0.05).to(cuda)
+    g = randn((4, 101 * 101), 95, torch.float32).to(cuda)
+    (gx,) = torch.autograd.grad(head(x, mask), (x,), g)
+    h64 = KeyQueryPolicyHead(384, 384).double()
+    h64.load_state_dict({n: t.double().cpu() for n, t in head.state_dict().items()})
+    x64 = x.detach().double().cpu().requires_grad_(True)
+    (want,) = torch.autograd.grad(h64(x64, mask.cpu()), (x64,), g.double().cpu())
+    err = (gx.double().cpu() - want).abs().max().item()
+    assert err <= 1e-4 * want.abs().max().item(), err
+
+
+def test_unsupported_dims_fall_back(cuda):
+    """A 16-bit dim above 128 that is not a multiple of 64: refused by the
+    kernel, differentiated by torch ops under autograd."""
+    qb = torch.randn(4, 100, 144, device=cuda, dtype=torch.bfloat16)
+    assert not ops.kq_policy_backward_supported(100, 144, torch.bfloat16)
     with pytest.raises(NotImplementedError):
         ops.kq_policy_backward(qb, qb, torch.zeros(4, 10000, device=cuda))
-    qa = q.clone().requires_grad_(True)
-    masked_policy_logits(qa, q, None).sum().backward()
-    assert torch.isfinite(qa.grad).all()
+    qa = qb.clone().requires_grad_(True)
+    masked_policy_logits(qa, qb, None).float().sum().backward()
+    assert torch.isfinite(qa.grad.float()).all()
