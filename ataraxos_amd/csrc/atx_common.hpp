@@ -128,14 +128,36 @@ __device__ inline float shfl_xor(float v, int mask) {
 }
 
 // Max / sum over the four lanes {l, l^16, l^32, l^48} that share an MFMA
-// output column.
+// output column, with gfx950's lane-swap instructions (no LDS round trip).
+// v_permlane16_swap a, b swaps the odd 16-lane rows of a with the even rows of
+// b; applied to two copies of v it leaves v[l] in one register and v[l ^ 16]
+// in the other (which one depends on l; max and the commutative add do not
+// see the order).  v_permlane32_swap pairs l and l ^ 32 the same way.  The
+// sum is (v[l] + v[l^16]) + (v[l^32] + v[l^48]) in every lane.  (Inline asm:
+// this compiler's builtins for these instructions return the first register
+// for both results.  The s_nops cover the VALU-write-to-permlane hazard on
+// each side, which the compiler does not track through asm.)
+__device__ inline void lane_swap16(uint32_t& a, uint32_t& b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ inline void lane_swap32(uint32_t& a, uint32_t& b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
 __device__ inline float colgroup_max(float v) {
-    v = fmaxf(v, shfl_xor(v, 16));
-    return fmaxf(v, shfl_xor(v, 32));
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    lane_swap16(a, b);
+    v = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    a = b = __builtin_bit_cast(uint32_t, v);
+    lane_swap32(a, b);
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
 }
 __device__ inline float colgroup_sum(float v) {
-    v += shfl_xor(v, 16);
-    return v + shfl_xor(v, 32);
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    lane_swap16(a, b);
+    v = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+    a = b = __builtin_bit_cast(uint32_t, v);
+    lane_swap32(a, b);
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
 }
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -185,6 +207,18 @@ __device__ inline lds_t* lds_base() {
 __device__ inline lds_t* lds_opaque(lds_t* p) {
     asm volatile("" : "+v"(p));
     return p;
+}
+
+// A value the compiler cannot see through (for values it would otherwise
+// hoist out of a loop and keep live across it): per-lane (VGPR) and
+// wave-uniform (SGPR) forms.
+__device__ inline int opaque_v(int x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+__device__ inline int opaque_s(int x) {
+    asm volatile("" : "+s"(x));
+    return x;
 }
 
 // Hand-off of LDS data between the lanes of one wave.  The hardware runs a

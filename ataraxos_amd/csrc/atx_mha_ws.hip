@@ -1,0 +1,539 @@
+// Fused multi-head self-attention layer, persistent with producer and
+// consumer waves (bf16 / fp16), for 6 heads of 64 (embed_dim 384) at 65 to
+// 101 positions -- C3's Move-network layer:
+//   Y = out_proj(attention(q_proj(X), k_proj(X), v_proj(X)))
+// (stratego/networks/attention.py:152-204 with key_value = None), with the
+// arithmetic of atx_mha.hip: the same rounding points (Q, K, V and O rounded
+// to the 16-bit type, fp32 accumulation, Y rounded once) and the same k order
+// of every accumulation, so both kernels give identical results.
+//
+// One workgroup per CU loops over the samples b = blockIdx.x + i * gridDim.x.
+// Its 8 waves take two roles, one wave of each role on every SIMD:
+//  * producers (waves 0..3) project: wave p computes feature tile p of Q_h, of
+//    K_h and of V_h ([Q|K|V]^T = W X^T; one X^T operand read from LDS feeds
+//    three MFMAs) for every position tile and stores them into LDS slot h & 1;
+//  * consumers (waves 4..7) attend over head h - 1 in slot (h - 1) & 1, query
+//    tiles c and c + 4 of wave 4 + c, writing O over the Q rows it came from.
+// So while one head's projections keep the MFMA pipes busy, the previous
+// head's softmax (VALU, LDS and latency bound) runs beside them on the same
+// SIMDs.  Every wave also owns 3 of the 24 feature tiles of Y in registers
+// and adds Wo[:, 64h ..] O_h^T into them one step after head h's attention.
+//
+// A sample takes 7 steps s = 0..6:
+//   1. all waves: out-projection of head s - 2 (slot s & 1); at step 0 of any
+//      sample but the workgroup's first, the previous sample's head 5, then
+//      that sample's Y store;
+//   2. producers, s < 6: the MFMAs of head s (registers only); s = 6: the next
+//      sample's X rows into LDS.  Consumers, s >= 1: attention of head s - 1;
+//   3. barrier; then, s < 6, producers store head s into slot s & 1, barrier.
+// Slot s & 1 was last read in step s's part 1 (the out-projection of head
+// s - 2) and before that by the attention of head s - 2 in step s - 1, both
+// before step s's first barrier; X was last read by the producers in step 5.
+//
+// LDS: X (L rows, swizzled as eoff), then per slot Q and K (L rows rounded up
+// to even) and V (32 ceil(NP / 2) rows).  Operand reads of the last position
+// tile run past the end of a buffer into the next one; those rows only reach
+// results that are dropped or replaced: Q rows past L give output rows past
+// L, which the bounds of y's buffer resource drop; key scores past L are set
+// to -inf before the softmax; V rows L .. are stored as zeros (rows past
+// 16 NP are zeroed once), so the probability-0 keys add exact zeros.  Each
+// MFMA output column depends only on its own position's operand column, so
+// the values read past a buffer (even non-finite ones) stay in those columns.
+#include <mutex>
+
+#include "atx_mha.hpp"
+
+namespace atx {
+
+namespace {
+
+constexpr int kWsH = 6;
+constexpr int kWsE = kWsH * kD;
+#ifndef ATX_MHA_WS_FTP
+#define ATX_MHA_WS_FTP 2
+#endif
+constexpr int kWsFTP = ATX_MHA_WS_FTP;  // Y feature tiles of a producer wave
+constexpr int kWsFTC = 6 - kWsFTP;    // Y feature tiles of a consumer wave
+#ifndef ATX_MHA_WS_PF
+#define ATX_MHA_WS_PF 2
+#endif
+constexpr int kWsPF = ATX_MHA_WS_PF;  // weight k-steps in flight in the projections
+
+constexpr int ws_lq(int L) { return (L + 1) & ~1; }
+constexpr int ws_lv(int np) { return 32 * ((np + 1) / 2); }
+constexpr size_t ws_slot(int L) { return (size_t)(2 * ws_lq(L) + ws_lv((L + 15) / 16)) * kD * 2; }
+constexpr size_t ws_lds(int L) { return (size_t)L * kWsE * 2 + 2 * ws_slot(L); }
+
+// Producer p, head h: feature tile p of Q_h, K_h and V_h for every position
+// tile, accumulated over the E inputs in 12 k-steps of 32.  The weight rows of
+// the three tiles sit at the same offset in the three matrices; weights run
+// kWsPF k-steps ahead of the MFMAs, and each X^T operand of the next k-step is
+// read right after the three MFMAs that used the same register, so an LDS
+// read's latency passes under the rest of the k-step.
+template <typename T, int NP, bool PK>
+__device__ __forceinline__ void ws_project(const lds_t* sx, int m, int g, const rsrc_t (&rw)[4], uint32_t wrow,
+                                           f32x4 (&acc)[3][NP]) {
+    using M = Mfma16<T>;
+    constexpr int KS = kWsE / 32;
+    constexpr int PF = kWsPF;
+    // X^T operand rows: logical chunk kk*4 + g of row pt*16 + m sits at
+    // xlane[kk & 3] + pt*16*E*2 + (kk >> 2)*256.
+    int xlane[4];
+#pragma unroll
+    for (int par = 0; par < 4; ++par) xlane[par] = m * kWsE * 2 + (((4 * par + g) ^ m) & 15) * 16;
+#pragma unroll
+    for (int f = 0; f < 3; ++f)
+#pragma unroll
+        for (int q = 0; q < NP; ++q) acc[f][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    u32x4 wbuf[PF][3];
+#pragma unroll
+    for (int q = 0; q < PF; ++q)
+#pragma unroll
+        for (int f = 0; f < 3; ++f) wbuf[q][f] = buf_ld16_keep(rw[f], wrow + q * kWStep<PK>);
+    u32x4 xb[NP];
+#pragma unroll
+    for (int q = 0; q < NP; ++q) xb[q] = lds_ld16(sx + xlane[0] + q * 16 * kWsE * 2);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+        u32x4 cur[3];
+#pragma unroll
+        for (int f = 0; f < 3; ++f) cur[f] = wbuf[kk % PF][f];
+        if (kk + PF < KS)
+#pragma unroll
+            for (int f = 0; f < 3; ++f) wbuf[kk % PF][f] = buf_ld16_keep(rw[f], wrow + (kk + PF) * kWStep<PK>);
+        // Scheduling barriers pin the loads where they are issued (the
+        // compiler would otherwise sink each one to its use and wait on it).
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+#pragma unroll
+            for (int f = 0; f < 3; ++f) acc[f][q] = M::mma(cur[f], xb[q], acc[f][q]);
+            if (kk + 1 < KS)
+                xb[q] = lds_ld16(sx + xlane[(kk + 1) & 3] + q * 16 * kWsE * 2 + ((kk + 1) >> 2) * 256);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+// Attention of one head for query tile qt (rows 16 qt .. 16 qt + 15), as
+// attend_tile computes it (S^T = K Q^T, row softmax in registers, O^T = V^T
+// P^T with V^T from transposing reads; same operations in the same order), with
+// the LDS reads issued ahead of their MFMAs: every K operand before the S^T
+// MFMAs, every V^T operand before the softmax.  Returns the lane's O elements
+// 16g .. 16g + 15 of row 16 qt + m, rounded to T, as two 16-byte chunks.
+template <typename T, int NP, bool CAUSAL>
+__device__ __forceinline__ void ws_attend_tile(const lds_t* sq, const lds_t* sk, const lds_t* sv, int qt, int L, float c2,
+                                               int m, int g, u32x4 (&out)[2]) {
+    using M = Mfma16<T>;
+    constexpr int NKC = (NP + 1) / 2;  // 32-key chunks
+    const float kNegInf = -__builtin_inff();
+    const int qrow = qt * 16 + m;
+    const int kend = CAUSAL ? min(L, qt * 16 + 16) : L;  // keys >= kend are unusable for the whole tile
+    // Without the causal mask every key tile (and 32-key chunk) below NP holds
+    // a key < L, since 16 (NP - 1) < L: those tests are then compile-time
+    // constants and the tiles' MFMAs form one straight-line block.  Only the
+    // last key tile can hold keys >= L.
+    const auto live = [&](int k0) { return !CAUSAL || k0 < kend; };
+    u32x4 qop[2], kop[NP][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) qop[i] = lds_ld16(sq + xoff<kD>(qrow, 4 * i + g));
+#pragma unroll
+    for (int kt = 0; kt < NP; ++kt)
+        if (live(kt * 16))
+#pragma unroll
+            for (int i = 0; i < 2; ++i) kop[kt][i] = lds_ld16(sk + xoff<kD>(kt * 16 + m, 4 * i + g));
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 sc[NP];
+    float mx = kNegInf;
+#pragma unroll
+    for (int kt = 0; kt < NP; ++kt) {
+        if (live(kt * 16)) {
+            f32x4 acc = M::mma(kop[kt][0], qop[0], f32x4{0.f, 0.f, 0.f, 0.f});
+            acc = M::mma(kop[kt][1], qop[1], acc);
+            if (CAUSAL ? kt * 16 + 16 > min(L, qt * 16 + 1) : kt == NP - 1) {
+                u32x4 ab = __builtin_bit_cast(u32x4, acc);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = kt * 16 + 4 * g + i;
+                    const bool ok = key < L && (!CAUSAL || key <= qrow);
+                    ab[i] = ok ? ab[i] : 0xff800000u;
+                }
+                acc = __builtin_bit_cast(f32x4, ab);
+            }
+            mx = fmaxf(fmaxf(mx, acc[0]), acc[1]);
+            mx = fmaxf(fmaxf(mx, acc[2]), acc[3]);
+            sc[kt] = acc;
+        }
+    }
+    // V^T operands (rows 4g + t of each 16-key half-chunk, elements
+    // (m & 3) * 16 + 4 dt), in flight during the softmax.
+    u32x2 vop[4][NKC][2];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+        const int troff = xquad<kD>(4 * g + (m >> 2), (m & 3) * 16 + 4 * dt);
+#pragma unroll
+        for (int c = 0; c < NKC; ++c)
+            if (live(c * 32))
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) vop[dt][c][hh] = lds_ld8_tr16(sv + (32 * c + 16 * hh) * kD * 2 + troff);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mx = colgroup_max(mx);
+    const float nb = -mx * c2;  // every query sees key 0: mx is finite
+    float sum = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < NP; ++kt) {
+        if (live(kt * 16)) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[kt][i] = fast_exp2(__builtin_fmaf(sc[kt][i], c2, nb));
+                sum += sc[kt][i];
+            }
+        }
+    }
+    sum = colgroup_sum(sum);
+    const float rs = 1.f / sum;
+    // P^T packed per 32-key chunk (unnormalised; 1/sum applied to O)
+    u32x4 pk[NKC];
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) {
+        float pv[8];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int kt = 2 * c + hh;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pv[4 * hh + i] = (kt < NP && live(kt * 16)) ? sc[kt < NP ? kt : 0][i] : 0.f;
+        }
+        pk[c] = u32x4{M::pack2(pv[0], pv[1]), M::pack2(pv[2], pv[3]), M::pack2(pv[4], pv[5]), M::pack2(pv[6], pv[7])};
+    }
+    // O^T = V^T P^T: lane m (query) gets d = 16g + 4dt + i
+    f32x4 o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NKC; ++c)
+            if (live(c * 32))
+                acc = M::mma(u32x4{vop[dt][c][0][0], vop[dt][c][0][1], vop[dt][c][1][0], vop[dt][c][1][1]}, pk[c], acc);
+        o[dt] = acc;
+    }
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+        out[half] = u32x4{M::pack2(o[2 * half][0] * rs, o[2 * half][1] * rs), M::pack2(o[2 * half][2] * rs, o[2 * half][3] * rs),
+                          M::pack2(o[2 * half + 1][0] * rs, o[2 * half + 1][1] * rs),
+                          M::pack2(o[2 * half + 1][2] * rs, o[2 * half + 1][3] * rs)};
+}
+
+// Producer p's tiles of head h (+ bias), rounded, into Q, K, V of the slot:
+// Q and K rows below L, V rows below L and zeros for rows L .. 16 NP - 1.
+template <typename T, int NP>
+__device__ __forceinline__ void ws_store(const f32x4 (&acc)[3][NP], lds_t* sq, lds_t* sk, lds_t* sv,
+                                         const void* const (&bias)[4], int h, int p, int L, int m, int g) {
+    using M = Mfma16<T>;
+#pragma unroll
+    for (int f = 0; f < 3; ++f) {
+        f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};  // bias of features 4g .. 4g+3 of the tile
+        const T* bp = static_cast<const T*>(bias[f]);
+        if (bp) {
+            const int feat = h * kD + p * 16 + 4 * g;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bv[i] = static_cast<float>(bp[feat + i]);
+        }
+        lds_t* const dst = f == 0 ? sq : (f == 1 ? sk : sv);
+#pragma unroll
+        for (int pt = 0; pt < NP; ++pt) {
+            const int row = pt * 16 + m;
+            const u32x2 v = u32x2{M::pack2(acc[f][pt][0] + bv[0], acc[f][pt][1] + bv[1]),
+                                  M::pack2(acc[f][pt][2] + bv[2], acc[f][pt][3] + bv[3])};
+            if (row < L)
+                lds_st8(dst + xquad<kD>(row, p * 16 + 4 * g), v);
+            else if (f == 2)
+                lds_st8(dst + xquad<kD>(row, p * 16 + 4 * g), u32x2{0u, 0u});
+        }
+    }
+}
+
+// Y feature tiles ft0 .. ft0 + FT - 1 (+ bias) of sample b, rounded once; rows
+// past L are dropped.
+template <typename T, int FT, int NP>
+__device__ __forceinline__ void ws_store_y(const f32x4 (&yacc)[FT][NP], const MhaArgs& a, int b, int ft0, int m, int g) {
+    using M = Mfma16<T>;
+    const int L = a.L;
+    const rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + b * a.ysb, (uint32_t)(((L - 1) * a.yss + kWsE) * 2));
+    const T* const bo = static_cast<const T*>(a.bias[3]);
+#pragma unroll
+    for (int f = 0; f < FT; ++f) {
+        const int feat = (ft0 + f) * 16 + 4 * g;
+        f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (bo)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bv[i] = static_cast<float>(bo[feat + i]);
+#pragma unroll
+        for (int q = 0; q < NP; ++q)
+            buf_st8_cached(ry, (uint32_t)((q * 16 + m) * a.yss + feat) * 2,
+                           u32x2{M::pack2(yacc[f][q][0] + bv[0], yacc[f][q][1] + bv[1]),
+                                 M::pack2(yacc[f][q][2] + bv[2], yacc[f][q][3] + bv[3])});
+    }
+}
+
+// X rows of sample b into LDS (swizzled), by NTHR threads (thread index t).
+template <typename T, int NP, int NTHR>
+__device__ __forceinline__ void ws_load_x(lds_t* sx, const MhaArgs& a, int b, int t) {
+    constexpr int XC = kWsE / 8;
+    constexpr int U = (NP * 16 * XC + NTHR - 1) / NTHR;
+    // Opaque copies: called inside the sample loop, the per-pass offsets
+    // would otherwise be hoisted out of it and held (or spilled) throughout.
+    const int L = opaque_s(a.L);
+    t = opaque_v(t);
+    const int N = L * XC;
+    const rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + b * a.xsb, (uint32_t)(((L - 1) * a.xss + kWsE) * 2));
+    u32x4 v[U];
+    // Whole passes are uniform branches; only the last pass tests its lanes.
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int idx = u * NTHR + t;
+        const int r = idx / XC, c = idx - (idx / XC) * XC;
+        if (u * NTHR < N) v[u] = buf_ld16(rx, idx < N ? (uint32_t)(r * a.xss + c * 8) * 2 : 0xfffffff0u);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int idx = u * NTHR + t;
+        const int r = idx / XC, c = idx - (idx / XC) * XC;
+        if (u * NTHR + NTHR <= N)
+            lds_st16(sx + eoff<kWsE>(r, c), v[u]);
+        else if (u * NTHR < N && idx < N)
+            lds_st16(sx + eoff<kWsE>(r, c), v[u]);
+    }
+}
+
+// Y^T += Wo[:, 64h ..] O_h^T for Y feature tiles ft0 .. ft0 + FT - 1: the Wo
+// operands of head h (two k-steps), loaded one step ahead of their use.
+template <int FT, bool PK>
+__device__ __forceinline__ void ws_load_wo(u32x4 (&wo)[2][FT], rsrc_t rwo, int ft0, int m, int g, int h) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int f = 0; f < FT; ++f)
+            wo[j][f] = buf_ld16_keep(rwo, wtile_off<kWsE, PK>(ft0 + f, m, g) + (uint32_t)(2 * h + j) * kWStep<PK>);
+}
+
+struct WsCtx {
+    lds_t* sx0;  // X
+    lds_t* ss0;  // slot 0 (slot 1 follows at +slot)
+    int slot;    // bytes per slot
+    int LQ;      // Q / K rows per slot
+    int lane;
+    int batch;
+};
+
+// Part 1 of step s (shared by both roles): the out-projection of head s - 2,
+// or at step 0 of every sample but the first that of the previous sample's
+// last head, followed by the previous sample's Y store.
+template <typename T, int FT, int NP>
+__device__ __forceinline__ void ws_out_proj(f32x4 (&yacc)[FT][NP], const u32x4 (&wo)[2][FT], const WsCtx& c, const MhaArgs& a,
+                                            int b, int s, int ft0, int m, int g) {
+    if (s >= 2 || (s == 0 && b != (int)blockIdx.x)) {
+        const int hh = s >= 2 ? s - 2 : kWsH - 1;
+        out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + (hh & 1) * c.slot, m, g);
+        if (s == 0) {
+            ws_store_y<T, FT, NP>(yacc, a, b - (int)gridDim.x, ft0, m, g);
+#pragma unroll
+            for (int f = 0; f < FT; ++f)
+#pragma unroll
+                for (int q = 0; q < NP; ++q) yacc[f][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+}
+
+// Producer wave p (0..3): owns Y feature tiles 2p, 2p + 1.
+template <typename T, int NP, bool PK>
+__device__ __forceinline__ void ws_producer(const WsCtx& c, const MhaArgs& a, const rsrc_t (&rw)[4], int p) {
+    constexpr int FT = kWsFTP;
+    const int ft0 = FT * p;
+    const int grid = gridDim.x;
+    f32x4 yacc[FT][NP];
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+        for (int q = 0; q < NP; ++q) yacc[f][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    u32x4 wo[2][FT];
+    for (int b = blockIdx.x; b < c.batch; b += grid) {
+        for (int s = 0; s <= kWsH; ++s) {
+            // Per-lane offsets and L are re-derived every step from opaque
+            // copies: hoisted out of the loops, the compiler would keep dozens
+            // of them (addresses, row < L tests) live throughout and spill.
+            const int ln = opaque_v(c.lane);
+            const int m = ln & 15, g = ln >> 4;
+            ws_out_proj<T, FT, NP>(yacc, wo, c, a, b, s, ft0, m, g);
+            if (s < kWsH) {
+                f32x4 acc[3][NP];
+                ws_project<T, NP, PK>(lds_opaque(c.sx0), m, g, rw, wtile_off<kWsE, PK>(s * 4 + p, m, g), acc);
+                // (Unconditional, so `wo` is dead during the projections: at
+                // step 0 this loads head 0's operands, which nothing uses.)
+                ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, s > 0 ? s - 1 : 0);
+                __syncthreads();
+                lds_t* const sq = lds_opaque(c.ss0) + (s & 1) * c.slot;
+                ws_store<T, NP>(acc, sq, sq + c.LQ * kD * 2, sq + 2 * c.LQ * kD * 2, a.bias, s, p, opaque_s(a.L), m, g);
+                __syncthreads();
+            } else {
+                if (b + grid < c.batch) ws_load_x<T, NP, 256>(lds_opaque(c.sx0), a, b + grid, p * 64 + ln);
+                ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, kWsH - 1);
+                __syncthreads();
+            }
+        }
+    }
+    const int m = c.lane & 15, g = c.lane >> 4;
+    const int last = blockIdx.x + ((c.batch - 1 - (int)blockIdx.x) / grid) * grid;
+    out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + ((kWsH - 1) & 1) * c.slot, m, g);
+    ws_store_y<T, FT, NP>(yacc, a, last, ft0, m, g);
+}
+
+// Consumer wave 4 + cq (cq 0..3): query tiles cq and cq + 4; owns Y feature
+// tiles 8 + 4 cq .. 8 + 4 cq + 3.
+template <typename T, int NP, bool CAUSAL, bool PK>
+__device__ __forceinline__ void ws_consumer(const WsCtx& c, const MhaArgs& a, const rsrc_t (&rw)[4], int cq) {
+    constexpr int FT = kWsFTC;
+    const int ft0 = 4 * kWsFTP + FT * cq;
+    const int grid = gridDim.x;
+    f32x4 yacc[FT][NP];
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+        for (int q = 0; q < NP; ++q) yacc[f][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    u32x4 wo[2][FT];
+    for (int b = blockIdx.x; b < c.batch; b += grid) {
+        for (int s = 0; s <= kWsH; ++s) {
+            const int ln = opaque_v(c.lane);
+            const int m = ln & 15, g = ln >> 4;
+            ws_out_proj<T, FT, NP>(yacc, wo, c, a, b, s, ft0, m, g);
+            if (s >= 1) {
+                const int L = opaque_s(a.L);
+                lds_t* const sq = lds_opaque(c.ss0) + ((s - 1) & 1) * c.slot;
+                lds_t* const sk = sq + c.LQ * kD * 2;
+                lds_t* const sv = sk + c.LQ * kD * 2;
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const int qt = cq + 4 * r;
+                    if (qt < NP) {
+                        u32x4 out[2];
+                        ws_attend_tile<T, NP, CAUSAL>(sq, sk, sv, qt, L, a.c2, m, g, out);
+                        if (qt * 16 + m < L)
+#pragma unroll
+                            for (int half = 0; half < 2; ++half) lds_st16(sq + xoff<kD>(qt * 16 + m, 2 * g + half), out[half]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, s > 0 ? s - 1 : 0);
+            __syncthreads();
+            if (s < kWsH) __syncthreads();  // the producers' stores
+        }
+    }
+    const int m = c.lane & 15, g = c.lane >> 4;
+    const int last = blockIdx.x + ((c.batch - 1 - (int)blockIdx.x) / grid) * grid;
+    out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + ((kWsH - 1) & 1) * c.slot, m, g);
+    ws_store_y<T, FT, NP>(yacc, a, last, ft0, m, g);
+}
+
+template <typename T, int NP, bool CAUSAL, bool PK>
+__global__ __launch_bounds__(kThreads) void mha_ws(MhaArgs a, int batch) {
+    constexpr int E = kWsE;
+    constexpr int LP = NP * 16;
+    constexpr int LV = ws_lv(NP);
+    static_assert(kWaves == 8, "wave roles assume 8 waves");
+    static_assert(4 * kWsFTP + 4 * kWsFTC == E / 16, "Y tiles split over the waves");
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    WsCtx c;
+    c.lane = tid & 63;
+    c.batch = batch;
+    c.LQ = ws_lq(a.L);
+    c.slot = (2 * c.LQ + LV) * kD * 2;
+    c.sx0 = lds_base();
+    c.ss0 = c.sx0 + a.L * E * 2;
+
+    rsrc_t rw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rw[i] = make_rsrc(a.w[i], (uint32_t)(E * E * 2));
+
+    // ---- first sample's X; V rows past 16 NP of both slots zeroed once -------------
+    ws_load_x<T, NP, kThreads>(c.sx0, a, blockIdx.x, tid);
+    for (int idx = tid; idx < 2 * (LV - LP) * 8; idx += kThreads) {
+        const int s = idx / ((LV - LP) * 8), j = idx - s * ((LV - LP) * 8);
+        lds_st16(c.ss0 + s * c.slot + 2 * c.LQ * kD * 2 + LP * kD * 2 + j * 16, u32x4{0, 0, 0, 0});
+    }
+    __syncthreads();
+
+    // The two roles run separate loops with the same barriers in the same
+    // order (the branch is uniform over each wave), each with its own
+    // registers.
+    if (wave < 4)
+        ws_producer<T, NP, PK>(c, a, rw, wave);
+    else
+        ws_consumer<T, NP, CAUSAL, PK>(c, a, rw, wave - 4);
+}
+
+template <typename K>
+int launch_ws(K kernel, int grid, int batch, size_t lds, hipStream_t st, const MhaArgs& a) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) ATX_FAIL(ATX_ERR_LAUNCH, "hipFuncSetAttribute(%zu bytes LDS): %s", lds, hipGetErrorString(e));
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), lds, st, a, batch);
+    ATX_CHECK_LAUNCH("atx_mha_fwd (persistent form) launch");
+    return ATX_OK;
+}
+
+template <typename T, bool CAUSAL, bool PK>
+int ws_np(int np, int grid, int batch, size_t lds, hipStream_t st, const MhaArgs& a) {
+    switch (np) {
+        case 5: return launch_ws(mha_ws<T, 5, CAUSAL, PK>, grid, batch, lds, st, a);
+        case 6: return launch_ws(mha_ws<T, 6, CAUSAL, PK>, grid, batch, lds, st, a);
+        case 7: return launch_ws(mha_ws<T, 7, CAUSAL, PK>, grid, batch, lds, st, a);
+        default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd (persistent form): %d position tiles", np);
+    }
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_cu_mu;
+int g_cu_count[kMaxDevices] = {};
+
+// Compute units of the current device (looked up once per device).
+int cu_count(int* out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) ATX_FAIL(ATX_ERR_LAUNCH, "atx_mha_fwd: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: device %d (at most %d devices)", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_cu_mu);
+    if (!g_cu_count[dev]) {
+        int n = 0;
+        e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess || n < 1)
+            ATX_FAIL(ATX_ERR_LAUNCH, "atx_mha_fwd: compute-unit count of device %d: %s", dev, hipGetErrorString(e));
+        g_cu_count[dev] = n;
+    }
+    *out = g_cu_count[dev];
+    return ATX_OK;
+}
+
+}  // namespace
+
+size_t mha_ws_lds_bytes(int E, int L) {
+    if (E != kWsE || L < 65 || L > 112) return 0;
+    const size_t lds = ws_lds(L);
+    return lds <= 160 * 1024 ? lds : 0;
+}
+
+int mha_ws_launch(int L, bool causal, bool bf16, bool packed, int batch, size_t lds, hipStream_t st, const MhaArgs& a) {
+    int ncu = 0;
+    if (const int rc = cu_count(&ncu)) return rc;
+    const int grid = batch < ncu ? batch : ncu;
+    const int np = (L + 15) / 16;
+    if (packed) {
+        if (bf16) return causal ? ws_np<__bf16, true, true>(np, grid, batch, lds, st, a) : ws_np<__bf16, false, true>(np, grid, batch, lds, st, a);
+        return causal ? ws_np<_Float16, true, true>(np, grid, batch, lds, st, a) : ws_np<_Float16, false, true>(np, grid, batch, lds, st, a);
+    }
+    if (bf16) return causal ? ws_np<__bf16, true, false>(np, grid, batch, lds, st, a) : ws_np<__bf16, false, false>(np, grid, batch, lds, st, a);
+    return causal ? ws_np<_Float16, true, false>(np, grid, batch, lds, st, a) : ws_np<_Float16, false, false>(np, grid, batch, lds, st, a);
+}
+
+}  // namespace atx

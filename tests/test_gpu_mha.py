@@ -347,3 +347,50 @@ def test_module_built_under_inference_mode(cuda):
         direct = ops.mha_forward(x, m.q_proj.weight, m.k_proj.weight, m.v_proj.weight, m.out_proj.weight, num_heads=6)
     assert not torch.equal(y0, y1)
     assert torch.equal(y1, direct)
+
+
+@pytest.mark.parametrize(
+    "b,l,dtype,causal,bias,packed,x_view",
+    [
+        (1, 100, torch.bfloat16, False, False, True, False),
+        (3, 65, torch.bfloat16, False, True, True, False),
+        (300, 100, torch.bfloat16, False, False, True, False),
+        (513, 101, torch.float16, False, True, False, False),
+        (257, 80, torch.bfloat16, True, False, True, True),
+        (40, 97, torch.float16, True, True, True, False),
+        (600, 96, torch.bfloat16, False, False, False, True),
+        (2, 81, torch.bfloat16, False, False, False, False),
+    ],
+)
+def test_persistent_form_equals_the_one_workgroup_per_sample_form(cuda, monkeypatch, b, l, dtype, causal, bias, packed, x_view):
+    """6 heads at 65-101 positions run the persistent producer/consumer kernel
+    (one workgroup per CU looping over samples).  It does the arithmetic of
+    the one-workgroup-per-sample kernel, which the float64 oracle pins above,
+    in the same order: the outputs are bit-identical.  Batches past the CU
+    count make workgroups run 2-3 samples; NaN guards around a strided x and
+    around y check that nothing outside the views is read or written."""
+    e = 384
+    _announce(f"mha persistent form b={b} l={l} {dtype} causal={causal} bias={bias} packed={packed} view={x_view}")
+    x = randn((b, l, e), 700 + l + b, dtype)
+    if x_view:
+        big = torch.full((b, l + 3, e + 64), float("nan"), dtype=dtype)
+        big[:, :l, :e] = x
+        xd = big.to(cuda)[:, :l, :e]
+    else:
+        xd = x.to(cuda)
+    ws, bs = layer(e, dtype, 701 + l, bias)
+    wd = [w.to(cuda) for w in ws]
+    if packed:
+        wd = [ops.mha_pack_weight(w) for w in wd]
+    bd = [t.to(cuda) if t is not None else None for t in bs]
+    kw = dict(num_heads=6, b_q=bd[0], b_k=bd[1], b_v=bd[2], b_o=bd[3], causal=causal, packed=packed)
+    outs = []
+    for form in ("1", "0"):
+        monkeypatch.setenv("ATX_MHA_PERSISTENT", form)
+        guard = torch.full((b, l + 2, e), 3.0, dtype=dtype, device=cuda)
+        ops.mha_forward(xd, *wd, out=guard[:, :l], **kw)
+        torch.cuda.synchronize()
+        assert (guard[:, l:] == 3.0).all(), "rows past the sequence were written"
+        outs.append(guard[:, :l].clone())
+    assert torch.isfinite(outs[0].float()).all()
+    assert torch.equal(outs[0], outs[1])
