@@ -254,26 +254,45 @@ __device__ __forceinline__ void ws_store(const f32x4 (&acc)[3][NP], lds_t* sq, l
 }
 
 // Y feature tiles ft0 .. ft0 + FT - 1 (+ bias) of sample b, rounded once; rows
-// past L are dropped.
+// past L are dropped.  In the MFMA layout a lane holds 4 consecutive features
+// (8 bytes) of one row per tile.  For each pair of tiles, two lane swaps
+// across the 16-lane groups (pairing groups 0,1 with 2,3, then 0 with 1 and 2
+// with 3) leave lane group g with features 8g .. 8g + 7 of the pair's 32, so
+// each store writes 16 bytes per lane and 64 contiguous bytes per row: half
+// the store instructions and write requests of 8-byte stores.
 template <typename T, int FT, int NP>
 __device__ __forceinline__ void ws_store_y(const f32x4 (&yacc)[FT][NP], const MhaArgs& a, int b, int ft0, int m, int g) {
+    static_assert(FT % 2 == 0, "tiles go out in pairs");
     using M = Mfma16<T>;
     const int L = a.L;
     const rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + b * a.ysb, (uint32_t)(((L - 1) * a.yss + kWsE) * 2));
     const T* const bo = static_cast<const T*>(a.bias[3]);
+    // Bias of features 16 (ft0 + f) + 4g .. + 3, read before any store (a
+    // wait for the loads would otherwise wait for the stores too).
+    f32x4 bv[FT];
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
-        const int feat = (ft0 + f) * 16 + 4 * g;
-        f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};
+        bv[f] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (bo)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) bv[i] = static_cast<float>(bo[feat + i]);
-#pragma unroll
-        for (int q = 0; q < NP; ++q)
-            buf_st8_cached(ry, (uint32_t)((q * 16 + m) * a.yss + feat) * 2,
-                           u32x2{M::pack2(yacc[f][q][0] + bv[0], yacc[f][q][1] + bv[1]),
-                                 M::pack2(yacc[f][q][2] + bv[2], yacc[f][q][3] + bv[3])});
+            for (int i = 0; i < 4; ++i) bv[f][i] = static_cast<float>(bo[(ft0 + f) * 16 + 4 * g + i]);
     }
+#pragma unroll
+    for (int fp = 0; fp < FT / 2; ++fp)
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+            const f32x4& ya = yacc[2 * fp][q];
+            const f32x4& yb = yacc[2 * fp + 1][q];
+            const f32x4& ba = bv[2 * fp];
+            const f32x4& bb = bv[2 * fp + 1];
+            uint32_t x0 = M::pack2(ya[0] + ba[0], ya[1] + ba[1]), x1 = M::pack2(ya[2] + ba[2], ya[3] + ba[3]);
+            uint32_t y0 = M::pack2(yb[0] + bb[0], yb[1] + bb[1]), y1 = M::pack2(yb[2] + bb[2], yb[3] + bb[3]);
+            lane_swap32(x0, y0);
+            lane_swap32(x1, y1);
+            lane_swap16(x0, y0);
+            lane_swap16(x1, y1);
+            buf_st16_cached(ry, (uint32_t)((q * 16 + m) * a.yss + (ft0 + 2 * fp) * 16 + 8 * g) * 2, u32x4{x0, x1, y0, y1});
+        }
 }
 
 // X rows of sample b into LDS (swizzled), by NTHR threads (thread index t).
@@ -303,6 +322,50 @@ __device__ __forceinline__ void ws_load_x(lds_t* sx, const MhaArgs& a, int b, in
             lds_st16(sx + eoff<kWsE>(r, c), v[u]);
         else if (u * NTHR < N && idx < N)
             lds_st16(sx + eoff<kWsE>(r, c), v[u]);
+    }
+}
+
+// The next sample's X rows in two halves for the producers (256 threads):
+// the loads go out right after the last head's projection MFMAs, into
+// registers, and land in LDS a step later, once every producer is done reading
+// the current X.  kWsXU loads per thread cover the longest sequence the kernel
+// takes (kWsMaxL rows).
+constexpr int kWsMaxL = 101;
+#ifndef ATX_MHA_WS_XEARLY
+#define ATX_MHA_WS_XEARLY 8
+#endif
+constexpr int kWsXEarly = ATX_MHA_WS_XEARLY;  // loads issued before the last head's store
+template <int NP>
+constexpr int ws_xu() {
+    return ((16 * NP < kWsMaxL ? 16 * NP : kWsMaxL) * (kWsE / 8) + 255) / 256;
+}
+template <typename T, int UX, int U0, int U1>
+__device__ __forceinline__ void ws_x_issue(u32x4 (&v)[UX], const MhaArgs& a, int b, int t) {
+    constexpr int XC = kWsE / 8;
+    const int L = opaque_s(a.L);
+    t = opaque_v(t);
+    const int N = L * XC;
+    const rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + b * a.xsb, (uint32_t)(((L - 1) * a.xss + kWsE) * 2));
+    // No branches (a load past the rows reads zero): registers defined on
+    // every path stay in registers across the code between issue and commit.
+#pragma unroll
+    for (int u = U0; u < U1; ++u) {
+        const int idx = u * 256 + t;
+        const int r = idx / XC, c = idx - (idx / XC) * XC;
+        v[u] = buf_ld16(rx, idx < N ? (uint32_t)(r * a.xss + c * 8) * 2 : 0xfffffff0u);
+    }
+}
+template <int UX>
+__device__ __forceinline__ void ws_x_commit(const u32x4 (&v)[UX], lds_t* sx, int L, int t) {
+    constexpr int XC = kWsE / 8;
+    L = opaque_s(L);
+    t = opaque_v(t);
+    const int N = L * XC;
+#pragma unroll
+    for (int u = 0; u < UX; ++u) {
+        const int idx = u * 256 + t;
+        const int r = idx / XC, c = idx - (idx / XC) * XC;
+        if (idx < N) lds_st16(sx + eoff<kWsE>(r, c), v[u]);
     }
 }
 
@@ -357,30 +420,56 @@ __device__ __forceinline__ void ws_producer(const WsCtx& c, const MhaArgs& a, co
 #pragma unroll
         for (int q = 0; q < NP; ++q) yacc[f][q] = f32x4{0.f, 0.f, 0.f, 0.f};
     u32x4 wo[2][FT];
+    // Steps 0 .. 4 in a loop; the last head's projection (step 5) and step 6
+    // are written out, so that the next sample's X, loaded at the end of
+    // step 5, is live only across them.
+    const auto project = [&](int b, int s, int m, int g, f32x4 (&acc)[3][NP]) {
+        ws_out_proj<T, FT, NP>(yacc, wo, c, a, b, s, ft0, m, g);
+        ws_project<T, NP, PK>(lds_opaque(c.sx0), m, g, rw, wtile_off<kWsE, PK>(s * 4 + p, m, g), acc);
+        // (Unconditional, so `wo` is dead during the projections: at step 0
+        // this loads head 0's operands, which nothing uses.)
+        ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, s > 0 ? s - 1 : 0);
+    };
+    const auto store = [&](int s, int m, int g, const f32x4 (&acc)[3][NP]) {
+        lds_t* const sq = lds_opaque(c.ss0) + (s & 1) * c.slot;
+        ws_store<T, NP>(acc, sq, sq + c.LQ * kD * 2, sq + 2 * c.LQ * kD * 2, a.bias, s, p, opaque_s(a.L), m, g);
+    };
     for (int b = blockIdx.x; b < c.batch; b += grid) {
-        for (int s = 0; s <= kWsH; ++s) {
-            // Per-lane offsets and L are re-derived every step from opaque
-            // copies: hoisted out of the loops, the compiler would keep dozens
-            // of them (addresses, row < L tests) live throughout and spill.
+        for (int s = 0; s < kWsH - 1; ++s) {
+            // Per-lane offsets are re-derived every step from an opaque copy:
+            // hoisted out of the loops, the compiler would keep dozens of
+            // them live throughout and spill.
             const int ln = opaque_v(c.lane);
             const int m = ln & 15, g = ln >> 4;
-            ws_out_proj<T, FT, NP>(yacc, wo, c, a, b, s, ft0, m, g);
-            if (s < kWsH) {
-                f32x4 acc[3][NP];
-                ws_project<T, NP, PK>(lds_opaque(c.sx0), m, g, rw, wtile_off<kWsE, PK>(s * 4 + p, m, g), acc);
-                // (Unconditional, so `wo` is dead during the projections: at
-                // step 0 this loads head 0's operands, which nothing uses.)
-                ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, s > 0 ? s - 1 : 0);
-                __syncthreads();
-                lds_t* const sq = lds_opaque(c.ss0) + (s & 1) * c.slot;
-                ws_store<T, NP>(acc, sq, sq + c.LQ * kD * 2, sq + 2 * c.LQ * kD * 2, a.bias, s, p, opaque_s(a.L), m, g);
-                __syncthreads();
-            } else {
-                if (b + grid < c.batch) ws_load_x<T, NP, 256>(lds_opaque(c.sx0), a, b + grid, p * 64 + ln);
-                ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, kWsH - 1);
-                __syncthreads();
-            }
+            f32x4 acc[3][NP];
+            project(b, s, m, g, acc);
+            __syncthreads();
+            store(s, m, g, acc);
+            __syncthreads();
         }
+        const int ln = opaque_v(c.lane);
+        const int m = ln & 15, g = ln >> 4;
+        const bool more = b + grid < c.batch;
+        // (After the last sample this re-reads its own X, unused: the issue
+        // stays branch-free.)
+        u32x4 xv[ws_xu<NP>()];
+        {
+            f32x4 acc[3][NP];
+            project(b, kWsH - 1, m, g, acc);
+            // (Part of the loads here; the rest once acc is stored.)
+            __builtin_amdgcn_sched_barrier(0);
+            ws_x_issue<T, ws_xu<NP>(), 0, kWsXEarly>(xv, a, more ? b + grid : b, p * 64 + ln);
+            __syncthreads();
+            store(kWsH - 1, m, g, acc);
+            __syncthreads();
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        ws_x_issue<T, ws_xu<NP>(), kWsXEarly, ws_xu<NP>()>(xv, a, more ? b + grid : b, p * 64 + ln);
+        __builtin_amdgcn_sched_barrier(0);
+        ws_out_proj<T, FT, NP>(yacc, wo, c, a, b, kWsH, ft0, m, g);
+        if (more) ws_x_commit<ws_xu<NP>()>(xv, lds_opaque(c.sx0), a.L, p * 64 + ln);
+        ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, kWsH - 1);
+        __syncthreads();
     }
     const int m = c.lane & 15, g = c.lane >> 4;
     const int last = blockIdx.x + ((c.batch - 1 - (int)blockIdx.x) / grid) * grid;
@@ -518,7 +607,7 @@ int cu_count(int* out) {
 }  // namespace
 
 size_t mha_ws_lds_bytes(int E, int L) {
-    if (E != kWsE || L < 65 || L > 112) return 0;
+    if (E != kWsE || L < 65 || L > kWsMaxL) return 0;
     const size_t lds = ws_lds(L);
     return lds <= 160 * 1024 ? lds : 0;
 }
