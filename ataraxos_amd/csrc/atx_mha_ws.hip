@@ -224,6 +224,118 @@ __device__ __forceinline__ void ws_attend_tile(const lds_t* sq, const lds_t* sk,
                           M::pack2(o[2 * half + 1][2] * rs, o[2 * half + 1][3] * rs)};
 }
 
+// Two query tiles qa, qb of one head at once (no causal mask): the steps of
+// ws_attend_tile for each tile, in the same order, with every K and V^T
+// operand read once for both and the two tiles' chains side by side.
+template <typename T, int NP>
+__device__ __forceinline__ void ws_attend_pair(const lds_t* sq, const lds_t* sk, const lds_t* sv, int qa, int qb, int L, float c2,
+                                               int m, int g, u32x4 (&outa)[2], u32x4 (&outb)[2]) {
+    using M = Mfma16<T>;
+    constexpr int NKC = (NP + 1) / 2;  // 32-key chunks
+    const float kNegInf = -__builtin_inff();
+    u32x4 qopa[2], qopb[2], kop[NP][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        qopa[i] = lds_ld16(sq + xoff<kD>(qa * 16 + m, 4 * i + g));
+        qopb[i] = lds_ld16(sq + xoff<kD>(qb * 16 + m, 4 * i + g));
+    }
+#pragma unroll
+    for (int kt = 0; kt < NP; ++kt)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) kop[kt][i] = lds_ld16(sk + xoff<kD>(kt * 16 + m, 4 * i + g));
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 sa[NP], sb[NP];
+    float mxa = kNegInf, mxb = kNegInf;
+#pragma unroll
+    for (int kt = 0; kt < NP; ++kt) {
+        f32x4 acca = M::mma(kop[kt][0], qopa[0], f32x4{0.f, 0.f, 0.f, 0.f});
+        f32x4 accb = M::mma(kop[kt][0], qopb[0], f32x4{0.f, 0.f, 0.f, 0.f});
+        acca = M::mma(kop[kt][1], qopa[1], acca);
+        accb = M::mma(kop[kt][1], qopb[1], accb);
+        if (kt == NP - 1) {  // the only key tile that can hold keys >= L
+            u32x4 ba = __builtin_bit_cast(u32x4, acca), bb = __builtin_bit_cast(u32x4, accb);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool ok = kt * 16 + 4 * g + i < L;
+                ba[i] = ok ? ba[i] : 0xff800000u;
+                bb[i] = ok ? bb[i] : 0xff800000u;
+            }
+            acca = __builtin_bit_cast(f32x4, ba);
+            accb = __builtin_bit_cast(f32x4, bb);
+        }
+        mxa = fmaxf(fmaxf(mxa, acca[0]), acca[1]);
+        mxa = fmaxf(fmaxf(mxa, acca[2]), acca[3]);
+        mxb = fmaxf(fmaxf(mxb, accb[0]), accb[1]);
+        mxb = fmaxf(fmaxf(mxb, accb[2]), accb[3]);
+        sa[kt] = acca;
+        sb[kt] = accb;
+    }
+    u32x2 vop[4][NKC][2];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+        const int troff = xquad<kD>(4 * g + (m >> 2), (m & 3) * 16 + 4 * dt);
+#pragma unroll
+        for (int c = 0; c < NKC; ++c)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) vop[dt][c][hh] = lds_ld8_tr16(sv + (32 * c + 16 * hh) * kD * 2 + troff);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mxa = colgroup_max(mxa);
+    mxb = colgroup_max(mxb);
+    const float nba = -mxa * c2, nbb = -mxb * c2;  // every query sees key 0: both maxima are finite
+    float suma = 0.f, sumb = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < NP; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sa[kt][i] = fast_exp2(__builtin_fmaf(sa[kt][i], c2, nba));
+            suma += sa[kt][i];
+            sb[kt][i] = fast_exp2(__builtin_fmaf(sb[kt][i], c2, nbb));
+            sumb += sb[kt][i];
+        }
+    suma = colgroup_sum(suma);
+    sumb = colgroup_sum(sumb);
+    const float rsa = 1.f / suma, rsb = 1.f / sumb;
+    u32x4 pka[NKC], pkb[NKC];
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) {
+        float pa[8], pb[8];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int kt = 2 * c + hh;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                pa[4 * hh + i] = kt < NP ? sa[kt < NP ? kt : 0][i] : 0.f;
+                pb[4 * hh + i] = kt < NP ? sb[kt < NP ? kt : 0][i] : 0.f;
+            }
+        }
+        pka[c] = u32x4{M::pack2(pa[0], pa[1]), M::pack2(pa[2], pa[3]), M::pack2(pa[4], pa[5]), M::pack2(pa[6], pa[7])};
+        pkb[c] = u32x4{M::pack2(pb[0], pb[1]), M::pack2(pb[2], pb[3]), M::pack2(pb[4], pb[5]), M::pack2(pb[6], pb[7])};
+    }
+    f32x4 oa[4], ob[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+        f32x4 acca = f32x4{0.f, 0.f, 0.f, 0.f}, accb = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NKC; ++c) {
+            const u32x4 v = u32x4{vop[dt][c][0][0], vop[dt][c][0][1], vop[dt][c][1][0], vop[dt][c][1][1]};
+            acca = M::mma(v, pka[c], acca);
+            accb = M::mma(v, pkb[c], accb);
+        }
+        oa[dt] = acca;
+        ob[dt] = accb;
+    }
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        outa[half] = u32x4{M::pack2(oa[2 * half][0] * rsa, oa[2 * half][1] * rsa), M::pack2(oa[2 * half][2] * rsa, oa[2 * half][3] * rsa),
+                           M::pack2(oa[2 * half + 1][0] * rsa, oa[2 * half + 1][1] * rsa),
+                           M::pack2(oa[2 * half + 1][2] * rsa, oa[2 * half + 1][3] * rsa)};
+        outb[half] = u32x4{M::pack2(ob[2 * half][0] * rsb, ob[2 * half][1] * rsb), M::pack2(ob[2 * half][2] * rsb, ob[2 * half][3] * rsb),
+                           M::pack2(ob[2 * half + 1][0] * rsb, ob[2 * half + 1][1] * rsb),
+                           M::pack2(ob[2 * half + 1][2] * rsb, ob[2 * half + 1][3] * rsb)};
+    }
+}
+
 // Producer p's tiles of head h (+ bias), rounded, into Q, K, V of the slot:
 // Q and K rows below L, V rows below L and zeros for rows L .. 16 NP - 1.
 template <typename T, int NP>
@@ -262,7 +374,6 @@ __device__ __forceinline__ void ws_store(const f32x4 (&acc)[3][NP], lds_t* sq, l
 // the store instructions and write requests of 8-byte stores.
 template <typename T, int FT, int NP>
 __device__ __forceinline__ void ws_store_y(const f32x4 (&yacc)[FT][NP], const MhaArgs& a, int b, int ft0, int m, int g) {
-    static_assert(FT % 2 == 0, "tiles go out in pairs");
     using M = Mfma16<T>;
     const int L = a.L;
     const rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + b * a.ysb, (uint32_t)(((L - 1) * a.yss + kWsE) * 2));
@@ -292,6 +403,14 @@ __device__ __forceinline__ void ws_store_y(const f32x4 (&yacc)[FT][NP], const Mh
             lane_swap16(x0, y0);
             lane_swap16(x1, y1);
             buf_st16_cached(ry, (uint32_t)((q * 16 + m) * a.yss + (ft0 + 2 * fp) * 16 + 8 * g) * 2, u32x4{x0, x1, y0, y1});
+        }
+    if constexpr (FT % 2 == 1)  // an odd last tile: 8 bytes per lane
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+            const f32x4& y = yacc[FT - 1][q];
+            const f32x4& bb = bv[FT - 1];
+            buf_st8_cached(ry, (uint32_t)((q * 16 + m) * a.yss + (ft0 + FT - 1) * 16 + 4 * g) * 2,
+                           u32x2{M::pack2(y[0] + bb[0], y[1] + bb[1]), M::pack2(y[2] + bb[2], y[3] + bb[3])});
         }
 }
 
@@ -408,7 +527,7 @@ __device__ __forceinline__ void ws_out_proj(f32x4 (&yacc)[FT][NP], const u32x4 (
     }
 }
 
-// Producer wave p (0..3): owns Y feature tiles 2p, 2p + 1.
+// Producer wave p (0..3): owns Y feature tiles kWsFTP p .. kWsFTP p + kWsFTP - 1.
 template <typename T, int NP, bool PK>
 __device__ __forceinline__ void ws_producer(const WsCtx& c, const MhaArgs& a, const rsrc_t (&rw)[4], int p) {
     constexpr int FT = kWsFTP;
@@ -477,8 +596,8 @@ __device__ __forceinline__ void ws_producer(const WsCtx& c, const MhaArgs& a, co
     ws_store_y<T, FT, NP>(yacc, a, last, ft0, m, g);
 }
 
-// Consumer wave 4 + cq (cq 0..3): query tiles cq and cq + 4; owns Y feature
-// tiles 8 + 4 cq .. 8 + 4 cq + 3.
+// Consumer wave 4 + cq (cq 0..3): query tiles cq and cq + 4; owns the kWsFTC
+// Y feature tiles from 4 kWsFTP + kWsFTC cq on.
 template <typename T, int NP, bool CAUSAL, bool PK>
 __device__ __forceinline__ void ws_consumer(const WsCtx& c, const MhaArgs& a, const rsrc_t (&rw)[4], int cq) {
     constexpr int FT = kWsFTC;
@@ -500,17 +619,27 @@ __device__ __forceinline__ void ws_consumer(const WsCtx& c, const MhaArgs& a, co
                 lds_t* const sq = lds_opaque(c.ss0) + ((s - 1) & 1) * c.slot;
                 lds_t* const sk = sq + c.LQ * kD * 2;
                 lds_t* const sv = sk + c.LQ * kD * 2;
+                const auto put = [&](int qt, const u32x4 (&out)[2]) {
+                    if (qt * 16 + m < L)
 #pragma unroll
-                for (int r = 0; r < 2; ++r) {
-                    const int qt = cq + 4 * r;
-                    if (qt < NP) {
-                        u32x4 out[2];
-                        ws_attend_tile<T, NP, CAUSAL>(sq, sk, sv, qt, L, a.c2, m, g, out);
-                        if (qt * 16 + m < L)
+                        for (int half = 0; half < 2; ++half) lds_st16(sq + xoff<kD>(qt * 16 + m, 2 * g + half), out[half]);
+                };
+                if (!CAUSAL && cq + 4 < NP) {
+                    u32x4 outa[2], outb[2];
+                    ws_attend_pair<T, NP>(sq, sk, sv, cq, cq + 4, L, a.c2, m, g, outa, outb);
+                    put(cq, outa);
+                    put(cq + 4, outb);
+                } else {
 #pragma unroll
-                            for (int half = 0; half < 2; ++half) lds_st16(sq + xoff<kD>(qt * 16 + m, 2 * g + half), out[half]);
+                    for (int r = 0; r < 2; ++r) {
+                        const int qt = cq + 4 * r;
+                        if (qt < NP) {
+                            u32x4 out[2];
+                            ws_attend_tile<T, NP, CAUSAL>(sq, sk, sv, qt, L, a.c2, m, g, out);
+                            put(qt, out);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
                     }
-                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
             ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, s > 0 ? s - 1 : 0);
