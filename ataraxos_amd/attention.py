@@ -17,13 +17,15 @@ Backends (``backend`` property, the slot of attention.py:122-146):
 * ``"hip"``  — tensors on a GPU: the fused HIP kernel (``ops.attention``).
   Its range is head_dim a multiple of 16 up to 128 and at most 256 keys;
   outside that the forward raises instead of switching to another path.
-  Self-attention without autograd (inference, self-play) with head_dim 64,
-  2/4/6/8 heads, no GQA, 16-bit and up to 128 positions runs the whole layer
-  -- projections, attention, output projection -- as one launch
+  Self-attention without autograd (inference, self-play) with head_dim 64
+  and 2/4/6/8 heads, or head_dim 48 with 8 heads (the reference Move
+  network's 384 = 8 x 48), no GQA, 16-bit and up to 128 positions runs the
+  whole layer -- projections, attention, output projection -- as one launch
   (``ops.mha_forward``, weights rearranged into its tile order by one more
   launch on every call) where that is faster, i.e. from the sequence length
-  :data:`FUSED_MIN_SEQ` gives for the head count; with autograd the
-  projections stay ``nn.Linear`` and the attention kernel's backward applies.
+  :data:`FUSED_MIN_SEQ` (:data:`FUSED_MIN_SEQ_D48`) gives for the head count;
+  with autograd the projections stay ``nn.Linear`` and the attention
+  kernel's backward applies.
 * ``"math"`` — tensors on the CPU, or training with ``dropout > 0`` (the
   kernel has no dropout, as the reference's FA3 backend has none:
   attention.py:134-138).  It keeps the semantics of attention.py:281-316.
@@ -40,7 +42,7 @@ import torch.nn.functional as F  # noqa: N812
 
 from . import ops
 
-__all__ = ["MultiHeadAttention", "math_attention", "FUSED_MIN_SEQ"]
+__all__ = ["MultiHeadAttention", "math_attention", "FUSED_MIN_SEQ", "FUSED_MIN_SEQ_D48"]
 
 # Shortest sequence at which the one-launch layer (ops.mha_forward with packed
 # weights) beats the unfused path (hipBLASLt projections + the attention
@@ -50,6 +52,10 @@ __all__ = ["MultiHeadAttention", "math_attention", "FUSED_MIN_SEQ"]
 # length, so the shortest sequences stay cheaper unfused: at 8 heads 158 us
 # fused against 116 us unfused at L=16, 191 against 198 at L=24.
 FUSED_MIN_SEQ = {2: 1, 4: 1, 6: 16, 8: 24}
+# The same at head_dim 48 (8 heads, embed_dim 384: the reference Move
+# network), measured at B=4096: 202 us fused against 153 us unfused at L=8,
+# 211 against 241 at L=16, 856 against 1631 at the network's L=101.
+FUSED_MIN_SEQ_D48 = {8: 16}
 
 
 def math_attention(
@@ -156,11 +162,14 @@ class MultiHeadAttention(nn.Module):
         """The one-launch layer applies: GPU, no autograd, no dropout to run,
         a shape the fused kernel covers, and a sequence long enough for it to
         beat the unfused path (:data:`FUSED_MIN_SEQ`)."""
-        if not self.fuse_layer or self.backend != "hip" or self.num_kv_heads != self.num_heads or self.head_dim != 64:
+        if not self.fuse_layer or self.backend != "hip" or self.num_kv_heads != self.num_heads:
+            return False
+        if self.head_dim not in (48, 64):
             return False
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
             return False
-        if x.shape[1] < FUSED_MIN_SEQ.get(self.num_heads, 1 << 30):
+        table = FUSED_MIN_SEQ if self.head_dim == 64 else FUSED_MIN_SEQ_D48
+        if x.shape[1] < table.get(self.num_heads, 1 << 30):
             return False
         w = self.q_proj.weight
         return x.dtype == w.dtype and ops.mha_forward_supported(self.embed_dim, self.num_heads, x.shape[1], x.dtype)

@@ -70,12 +70,13 @@ inline size_t mha_lds_bytes(int E, int np) {
 // serves both tiles), the weight rows from memory with the next k-step in
 // flight.  Results (+ bias) are rounded and stored row-major into sq / sk / sv
 // after a workgroup barrier (all waves call this once per head).
-template <typename T, int E, int NP, int NF, int PB1, int PN1, bool PK>
+template <typename T, int E, int NP, int NF, int PB1, int PN1, bool PK, int D = kD>
 __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* sk, lds_t* sv, const int (&xlane)[4],
                                              rsrc_t rq, rsrc_t rk, rsrc_t rv, const void* const (&bias)[4], int h,
                                              int H, int fta, int ftb, int m, int g, u32x4 (&wpre)[NF]) {
     using M = Mfma16<T>;
     constexpr int KS = E / 32;
+    constexpr int TPH = D / 16;  // feature tiles per head in each of Q, K, V
     // tile f covers position tile p
     auto covers = [](int f, int p) constexpr { return f == 0 || (p >= PB1 && p < PB1 + PN1); };
     f32x4 acc[NF][NP];
@@ -88,8 +89,8 @@ __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* 
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
         const int ft = f == 0 ? fta : ftb;
-        wr[f] = (ft >> 2) == 0 ? rq : ((ft >> 2) == 1 ? rk : rv);
-        wrow[f] = wtile_off<E, PK>(h * 4 + (ft & 3), m, g);
+        wr[f] = ft / TPH == 0 ? rq : (ft / TPH == 1 ? rk : rv);
+        wrow[f] = wtile_off<E, PK>(h * TPH + ft % TPH, m, g);
     }
     // Weight k-steps stay PF ahead of the MFMAs: each iteration issues step
     // kk + PF first, and a scheduling barrier keeps the compiler from
@@ -128,44 +129,49 @@ __device__ __forceinline__ void project_head(const lds_t* sx, lds_t* sq, lds_t* 
 #pragma unroll
             for (int f = 0; f < NF; ++f) wbuf[kk % PF][f] = nxt[f];
     }
-    // Step 0 of head h + 1 (its rows start kD rows further down).
+    // Step 0 of head h + 1 (its rows start D rows further down).
     if (WPRE && h + 1 < H)
 #pragma unroll
-        for (int f = 0; f < NF; ++f) wpre[f] = buf_ld16_keep(wr[f], wrow[f] + kD * E * 2);
+        for (int f = 0; f < NF; ++f) wpre[f] = buf_ld16_keep(wr[f], wrow[f] + D * E * 2);
     __syncthreads();  // every wave is done with the previous head's Q, K, V
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
         const int ft = f == 0 ? fta : ftb;
         f32x4 bv = f32x4{0.f, 0.f, 0.f, 0.f};  // bias of features 4g .. 4g+3 of the tile
-        const T* bp = static_cast<const T*>(bias[ft >> 2]);
+        const T* bp = static_cast<const T*>(bias[ft / TPH]);
         if (bp) {
-            const int feat = h * kD + (ft & 3) * 16 + 4 * g;
+            const int feat = h * D + (ft % TPH) * 16 + 4 * g;
 #pragma unroll
             for (int i = 0; i < 4; ++i) bv[i] = static_cast<float>(bp[feat + i]);
         }
-        lds_t* const dst = ft < 4 ? sq : (ft < 8 ? sk : sv);
+        lds_t* const dst = ft < TPH ? sq : (ft < 2 * TPH ? sk : sv);
 #pragma unroll
         for (int p = 0; p < NP; ++p)
             if (covers(f, p))
-            lds_st8(dst + xquad<kD>(p * 16 + m, (ft & 3) * 16 + 4 * g),
+            lds_st8(dst + xquad<kD>(p * 16 + m, (ft % TPH) * 16 + 4 * g),
                     u32x2{M::pack2(acc[f][p][0] + bv[0], acc[f][p][1] + bv[1]),
                           M::pack2(acc[f][p][2] + bv[2], acc[f][p][3] + bv[3])});
     }
 }
 
-// H heads (even), NP 16-row position tiles (L <= 16 NP).
-template <typename T, int H, int NP, bool CAUSAL, bool PK>
+// H heads of D (64, or 48 with 8 heads), NP 16-row position tiles (L <= 16 NP).
+// With D = 48 the head's Q, K, V rows keep the 64-element LDS rows of D = 64
+// with elements 48 .. 63 zero, so the attention runs unchanged (the padded
+// dot-product terms and output columns are exact zeros; those columns are
+// not stored), and O always takes the parked form.
+template <typename T, int H, int NP, bool CAUSAL, bool PK, int D = kD>
 __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
     using M = Mfma16<T>;
-    constexpr int E = H * kD;
+    static_assert(D == kD || (D == 48 && H == 8), "head_dim 64, or 48 with 8 heads");
+    constexpr int E = H * D;
     constexpr int LP = NP * 16;
     constexpr int NKC = (NP + 1) / 2;  // 32-key chunks
     constexpr int LV = NKC * 32;       // V rows staged
     constexpr int KS = E / 32;         // k-steps of a projection
-    constexpr int FT = H / 2;          // output feature tiles of a wave
+    constexpr int FT = E / 128;        // output feature tiles of a wave (E / 16 over 8 waves)
     constexpr int PF = KS < PFD ? KS : PFD;  // weight prefetch depth (k-steps)
     constexpr int XC = E / 8;          // 16-byte chunks per X row
-    constexpr bool YREG = mha_y_in_regs(H, NP);
+    constexpr bool YREG = D == kD && mha_y_in_regs(H, NP);
     static_assert(H % 2 == 0 && H <= 8, "H even, at most 8");
     static_assert(kWaves == 8, "wave roles assume 8 waves");
 
@@ -202,6 +208,11 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
         }
         for (int idx = tid; idx < (LV - LP) * 8; idx += kThreads)
             lds_st16(sv0 + LP * kD * 2 + idx * 16, u32x4{0, 0, 0, 0});
+        if constexpr (D < kD)  // elements D .. 63 of every Q, K and V row: zero, never written
+            for (int idx = tid; idx < (2 * LP + LV) * (kD - D) / 8; idx += kThreads) {
+                const int r = idx / ((kD - D) / 8), c = D / 8 + idx % ((kD - D) / 8);
+                lds_st16(sq0 + xoff<kD>(r, c), u32x4{0, 0, 0, 0});
+            }
     }
 
     const rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + b * a.ysb, (uint32_t)(((L - 1) * a.yss + E) * 2));
@@ -249,10 +260,18 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
         // (Q, K), waves 4..7 tile 4 + w (V), each for every position, so every
         // weight element crosses from L2 once per sample and each SIMD holds
         // one 2-tile and one 1-tile wave.
-        if (wave < 4)
-            project_head<T, E, NP, 2, 0, NP, PK>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, H, 2 * wave, 2 * wave + 1, m, g, wpre);
-        else
-            project_head<T, E, NP, 1, 0, 0, PK>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, H, 4 + wave, 0, m, g, wpre1);
+        if constexpr (D == kD) {
+            if (wave < 4)
+                project_head<T, E, NP, 2, 0, NP, PK>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, H, 2 * wave, 2 * wave + 1, m, g, wpre);
+            else
+                project_head<T, E, NP, 1, 0, 0, PK>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, H, 4 + wave, 0, m, g, wpre1);
+        } else {
+            // 9 feature tiles (Q 0-2, K 3-5, V 6-8): wave w owns tile w, wave 0 also tile 8.
+            if (wave == 0)
+                project_head<T, E, NP, 2, 0, NP, PK, D>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, H, 0, 8, m, g, wpre);
+            else
+                project_head<T, E, NP, 1, 0, 0, PK, D>(sx, sq, sk, sv, xlane, rw[0], rw[1], rw[2], a.bias, h, H, wave, 0, m, g, wpre1);
+        }
         __syncthreads();
 
         // ---- B: attention of head h, one query tile per wave -------------------
@@ -283,9 +302,10 @@ __global__ __launch_bounds__(kThreads) void mha_fused(MhaArgs a) {
             if (wave < NP) {
                 u32x4 out[2];
                 attend_tile<T, NP, CAUSAL>(sq, sk, sv, troff, wave, L, a.c2, m, g, out);
+                if (16 * g < D)
 #pragma unroll
-                for (int half = 0; half < 2; ++half)
-                    buf_st16_cached(ry, (uint32_t)((wave * 16 + m) * a.yss + h * kD + 16 * g + 8 * half) * 2, out[half]);
+                    for (int half = 0; half < 2; ++half)
+                        buf_st16_cached(ry, (uint32_t)((wave * 16 + m) * a.yss + h * D + 16 * g + 8 * half) * 2, out[half]);
             }
         }
     }
@@ -384,23 +404,28 @@ int launch_mha(K kernel, int grid, size_t lds, hipStream_t st, const MhaArgs& a)
     return ATX_OK;
 }
 
-template <typename T, int H, bool CAUSAL, bool PK>
+template <typename T, int H, bool CAUSAL, bool PK, int D = kD>
 int dispatch_mha_np(int np, int grid, size_t lds, hipStream_t st, const MhaArgs& a) {
     switch (np) {
-        case 1: return launch_mha(mha_fused<T, H, 1, CAUSAL, PK>, grid, lds, st, a);
-        case 2: return launch_mha(mha_fused<T, H, 2, CAUSAL, PK>, grid, lds, st, a);
-        case 3: return launch_mha(mha_fused<T, H, 3, CAUSAL, PK>, grid, lds, st, a);
-        case 4: return launch_mha(mha_fused<T, H, 4, CAUSAL, PK>, grid, lds, st, a);
-        case 5: return launch_mha(mha_fused<T, H, 5, CAUSAL, PK>, grid, lds, st, a);
-        case 6: return launch_mha(mha_fused<T, H, 6, CAUSAL, PK>, grid, lds, st, a);
-        case 7: return launch_mha(mha_fused<T, H, 7, CAUSAL, PK>, grid, lds, st, a);
-        case 8: return launch_mha(mha_fused<T, H, 8, CAUSAL, PK>, grid, lds, st, a);
+        case 1: return launch_mha(mha_fused<T, H, 1, CAUSAL, PK, D>, grid, lds, st, a);
+        case 2: return launch_mha(mha_fused<T, H, 2, CAUSAL, PK, D>, grid, lds, st, a);
+        case 3: return launch_mha(mha_fused<T, H, 3, CAUSAL, PK, D>, grid, lds, st, a);
+        case 4: return launch_mha(mha_fused<T, H, 4, CAUSAL, PK, D>, grid, lds, st, a);
+        case 5: return launch_mha(mha_fused<T, H, 5, CAUSAL, PK, D>, grid, lds, st, a);
+        case 6: return launch_mha(mha_fused<T, H, 6, CAUSAL, PK, D>, grid, lds, st, a);
+        case 7: return launch_mha(mha_fused<T, H, 7, CAUSAL, PK, D>, grid, lds, st, a);
+        case 8: return launch_mha(mha_fused<T, H, 8, CAUSAL, PK, D>, grid, lds, st, a);
         default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: %d position tiles", np);
     }
 }
 
+// head_dim 64: 2, 4, 6 or 8 heads; head_dim 48: 8 heads (embed_dim 384).
 template <typename T, bool CAUSAL, bool PK>
-int dispatch_mha(int H, int np, int grid, size_t lds, hipStream_t st, const MhaArgs& a) {
+int dispatch_mha(int H, int D, int np, int grid, size_t lds, hipStream_t st, const MhaArgs& a) {
+    if (D == 48) {
+        if (H == 8) return dispatch_mha_np<T, 8, CAUSAL, PK, 48>(np, grid, lds, st, a);
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd: head_dim 48 with %d heads (8 only)", H);
+    }
     switch (H) {
         case 2: return dispatch_mha_np<T, 2, CAUSAL, PK>(np, grid, lds, st, a);
         case 4: return dispatch_mha_np<T, 4, CAUSAL, PK>(np, grid, lds, st, a);
@@ -428,8 +453,9 @@ int mha_check(const AtxMhaParams* p, const char* fn, MhaArgs& a, int& np, size_t
     }
     if (p->batch < 1 || p->seq < 1 || p->num_heads < 1)
         ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: sizes must be >= 1", fn);
-    if (p->embed_dim != p->num_heads * 64)
-        ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: head_dim %d not supported (64)", fn,
+    const bool d48 = p->num_heads == 8 && p->embed_dim == 384;  // the reference Move network's 8 x 48
+    if (p->embed_dim != p->num_heads * 64 && !d48)
+        ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: head_dim %d not supported (64; 48 with 8 heads)", fn,
                  p->num_heads > 0 ? p->embed_dim / p->num_heads : 0);
     if (p->num_heads != 2 && p->num_heads != 4 && p->num_heads != 6 && p->num_heads != 8)
         ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: %d heads not supported (2, 4, 6, 8)", fn, p->num_heads);
@@ -449,7 +475,7 @@ int mha_check(const AtxMhaParams* p, const char* fn, MhaArgs& a, int& np, size_t
         (int64_t)(L + 16) * yss * 2 + E * 2 > 0x7fffffffLL)
         ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: row strides must be >= 0 (y: >= embed_dim) and one sample < 2 GiB", fn);
     np = (L + 15) / 16;
-    lds = mha_lds_bytes(E, np);
+    lds = d48 ? mha_lds_core(E, np) : mha_lds_bytes(E, np);  // head_dim 48: O parked, no O buffers
     if (lds > 160 * 1024)
         ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: seq %d, embed_dim %d need %zu bytes of LDS (> 160 KiB)", fn, L, E, lds);
 
@@ -464,23 +490,25 @@ int mha_check(const AtxMhaParams* p, const char* fn, MhaArgs& a, int& np, size_t
 
 int mha_launch(const AtxMhaParams* p, const MhaArgs& a, int np, size_t lds, hipStream_t st, bool packed) {
     const int H = p->num_heads;
+    const int D = p->embed_dim / H;
     const bool bf = p->dtype == ATX_DTYPE_BF16;
-    // The persistent form where it applies, unless ATX_MHA_PERSISTENT=0 (both
-    // forms give identical results; the switch exists to compare them).
-    if (const size_t wl = mha_ws_lds_bytes(p->embed_dim, p->seq)) {
+    // The persistent form (6 heads of 64) where it applies, unless
+    // ATX_MHA_PERSISTENT=0 (both forms give identical results; the switch
+    // exists to compare them).
+    if (const size_t wl = H == 6 && D == kD ? mha_ws_lds_bytes(p->embed_dim, p->seq) : 0) {
         const char* env = getenv("ATX_MHA_PERSISTENT");
         if (!env || strcmp(env, "0") != 0) return mha_ws_launch(p->seq, p->causal != 0, bf, packed, p->batch, wl, st, a);
     }
     if (packed) {
-        if (bf) return p->causal ? dispatch_mha<__bf16, true, true>(H, np, p->batch, lds, st, a)
-                                 : dispatch_mha<__bf16, false, true>(H, np, p->batch, lds, st, a);
-        return p->causal ? dispatch_mha<_Float16, true, true>(H, np, p->batch, lds, st, a)
-                         : dispatch_mha<_Float16, false, true>(H, np, p->batch, lds, st, a);
+        if (bf) return p->causal ? dispatch_mha<__bf16, true, true>(H, D, np, p->batch, lds, st, a)
+                                 : dispatch_mha<__bf16, false, true>(H, D, np, p->batch, lds, st, a);
+        return p->causal ? dispatch_mha<_Float16, true, true>(H, D, np, p->batch, lds, st, a)
+                         : dispatch_mha<_Float16, false, true>(H, D, np, p->batch, lds, st, a);
     }
-    if (bf) return p->causal ? dispatch_mha<__bf16, true, false>(H, np, p->batch, lds, st, a)
-                             : dispatch_mha<__bf16, false, false>(H, np, p->batch, lds, st, a);
-    return p->causal ? dispatch_mha<_Float16, true, false>(H, np, p->batch, lds, st, a)
-                     : dispatch_mha<_Float16, false, false>(H, np, p->batch, lds, st, a);
+    if (bf) return p->causal ? dispatch_mha<__bf16, true, false>(H, D, np, p->batch, lds, st, a)
+                             : dispatch_mha<__bf16, false, false>(H, D, np, p->batch, lds, st, a);
+    return p->causal ? dispatch_mha<_Float16, true, false>(H, D, np, p->batch, lds, st, a)
+                     : dispatch_mha<_Float16, false, false>(H, D, np, p->batch, lds, st, a);
 }
 
 int mha_fwd(const AtxMhaParams* p, void* stream, bool packed) {

@@ -475,11 +475,12 @@ def _mha_lds_bytes(embed_dim: int, seq: int) -> int:
 
 def mha_forward_supported(embed_dim: int, num_heads: int, seq: int, dtype: torch.dtype) -> bool:
     """True when :func:`mha_forward` covers this layer: bf16/fp16, head_dim
-    64, 2/4/6/8 heads, up to 128 positions within 160 KiB of LDS."""
+    64 with 2/4/6/8 heads, or head_dim 48 with 8 heads (embed_dim 384, the
+    reference Move network), up to 128 positions within 160 KiB of LDS."""
     return (
         dtype in _BWD_DTYPES
         and num_heads in MHA_HEADS
-        and embed_dim == 64 * num_heads
+        and (embed_dim == 64 * num_heads or (num_heads == 8 and embed_dim == 384))
         and 1 <= seq <= 128
         and _mha_lds_bytes(embed_dim, seq) <= _LDS_BYTES
     )
@@ -551,7 +552,7 @@ def mha_forward(
     else:
         _check_out("mha_forward", out, (b, l, e), x.dtype, x.device)
     if scale is None:
-        scale = 1.0 / 8.0  # 1 / sqrt(head_dim = 64)
+        scale = 1.0 / math.sqrt(e // num_heads)  # 1 / sqrt(head_dim)
 
     p = _lib.MhaParams()
     p.abi_version = _lib.ABI_VERSION

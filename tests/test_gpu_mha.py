@@ -37,9 +37,9 @@ def layer(e, dtype, seed, bias=False):
     return ws, bs
 
 
-def run_case(cuda, b, l, h, dtype=torch.bfloat16, causal=False, bias=False, seed=0, x_view=False, packed=False):
-    e = 64 * h
-    _announce(f"mha b={b} l={l} h={h} {dtype} causal={causal} bias={bias} view={x_view} packed={packed}")
+def run_case(cuda, b, l, h, dtype=torch.bfloat16, causal=False, bias=False, seed=0, x_view=False, packed=False, d=64):
+    e = d * h
+    _announce(f"mha b={b} l={l} h={h}x{d} {dtype} causal={causal} bias={bias} view={x_view} packed={packed}")
     x = randn((b, l, e), seed, dtype)
     ws, bs = layer(e, dtype, seed + 1, bias)
     if x_view:  # rows of a wider buffer, NaN after the sequence and in the padding columns
@@ -394,3 +394,68 @@ def test_persistent_form_equals_the_one_workgroup_per_sample_form(cuda, monkeypa
         outs.append(guard[:, :l].clone())
     assert torch.isfinite(outs[0].float()).all()
     assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize(
+    "b,l,dtype,causal,bias,packed,x_view",
+    [
+        (4, 101, torch.bfloat16, False, False, True, False),
+        (3, 101, torch.bfloat16, False, True, False, False),
+        (3, 100, torch.float16, False, False, True, True),
+        (5, 1, torch.bfloat16, False, False, True, False),
+        (3, 17, torch.bfloat16, True, False, False, False),
+        (2, 40, torch.float16, True, True, True, False),
+        (3, 64, torch.bfloat16, False, False, True, False),
+        (2, 128, torch.bfloat16, True, True, True, False),
+    ],
+)
+def test_head_dim_48_reference_move_layer(cuda, b, l, dtype, causal, bias, packed, x_view):
+    """The reference Move network's layer, MultiHeadAttention(384, 8) with
+    head_dim 48 (constants.py:149-150, move_net.py:142-149) at its 101
+    tokens and other lengths, against the float64 oracle (scale 1/sqrt(48))."""
+    run_case(cuda, b, l, 8, dtype=dtype, causal=causal, bias=bias, seed=800 + l, x_view=x_view, packed=packed, d=48)
+
+
+def test_head_dim_48_module_takes_the_fused_layer(cuda, monkeypatch):
+    """MultiHeadAttention(384, 8) in inference at L=101 runs the one-launch
+    layer (no separate q/k/v projection), and equals the unfused module path
+    within the 16-bit tolerance."""
+    _announce("mha module 8x48 fused path")
+    torch.manual_seed(11)
+    m = MultiHeadAttention(384, 8).to(cuda, torch.bfloat16).eval()
+    x = randn((6, 101, 384), 74, torch.bfloat16).to(cuda)
+    calls = []
+    real = ops.mha_forward
+    monkeypatch.setattr(ops, "mha_forward", lambda *a, **k: calls.append(1) or real(*a, **k))
+    with torch.no_grad():
+        fused = m(x)
+        m.fuse_layer = False
+        unfused = m(x)
+    torch.cuda.synchronize()
+    assert calls, "the module did not take the fused layer"
+    names = ("q_proj", "k_proj", "v_proj", "out_proj")
+    weights = {f"{n}.weight": to_np64(getattr(m, n).weight) for n in names}
+    ref = oracle_mha(to_np64(x), None, weights, 8)
+    for y in (fused, unfused):
+        err = float(np.max(np.abs(to_np64(y) - ref)))
+        assert err <= 2e-2 * max(1.0, float(np.max(np.abs(ref)))), err
+
+
+def test_head_dim_48_full_batch_sampled_rows(cuda):
+    """B=4096 at the reference Move network's shape (L=101, 8 x 48), one
+    launch; sampled rows against the float64 oracle on those rows alone."""
+    b, l, e = 4096, 101, 384
+    _announce(f"mha 8x48 full batch b={b} l={l}")
+    x = randn((b, l, e), 810, torch.bfloat16)
+    ws, _ = layer(e, torch.bfloat16, 811)
+    xd = x.to(cuda)
+    y = ops.mha_forward(xd, *[ops.mha_pack_weight(w.to(cuda)) for w in ws], num_heads=8, packed=True)
+    torch.cuda.synchronize()
+    rows = [0, 1, 255, 256, 2047, 4095] + list(range(77, 4000, 613))
+    names = ("q_proj", "k_proj", "v_proj", "out_proj")
+    weights = {f"{n}.weight": to_np64(w) for n, w in zip(names, ws)}
+    ref = oracle_mha(to_np64(x[rows]), None, weights, 8)
+    got = to_np64(y[rows])
+    err = float(np.max(np.abs(got - ref)))
+    assert np.isfinite(got).all()
+    assert err <= 2e-2, err
