@@ -9,6 +9,9 @@
   :class:`BeliefDecoder` a Belief network with its encoder run once.
 * :func:`use_hip_attention` / :class:`KernelMultiheadAttention` — the Belief
   network's ``nn.TransformerDecoder`` attention through the same kernel.
+* :class:`PreLNTransformerBlock` / :class:`TransformerStack` — drop-ins for
+  the reference's pre-LN blocks; the attention half (LayerNorm, projections,
+  attention, residual) is one launch where the persistent kernel applies.
 * :class:`StrategoRolloutBuffer` — drop-in for the reference's CUDA self-play
   simulator: N games on the GPU producing the legal-move masks and
   infostates the networks consume.
@@ -22,6 +25,7 @@ from .decode import BeliefDecoder, KVCache, SetupDecoder
 from .decoder import KernelMultiheadAttention, use_hip_attention
 from .policy import KeyQueryPolicyHead, masked_policy_logits, masked_policy_softmax
 from .rollout import StrategoRolloutBuffer
+from .transformer import PreLNTransformerBlock, TransformerStack
 
 __all__ = [
     "ops",
@@ -36,4 +40,6 @@ __all__ = [
     "KernelMultiheadAttention",
     "use_hip_attention",
     "StrategoRolloutBuffer",
+    "PreLNTransformerBlock",
+    "TransformerStack",
 ]

@@ -14,7 +14,7 @@ import os
 import threading
 from pathlib import Path
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK = 0
 ERR_INVALID_ARGUMENT = -1
@@ -149,6 +149,10 @@ class MhaParams(ctypes.Structure):
         ("y_stride_b", _i64),
         ("y_stride_s", _i64),
         ("scale", _f32),
+        ("ln_weight", _ptr),
+        ("ln_bias", _ptr),
+        ("ln_eps", _f32),
+        ("residual", _i32),
     ]
 
 

@@ -143,6 +143,20 @@ __device__ inline void lane_swap16(uint32_t& a, uint32_t& b) {
 __device__ inline void lane_swap32(uint32_t& a, uint32_t& b) {
     asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
 }
+// Sum over the 16 lanes of a row (lanes 16r .. 16r + 15), every lane getting
+// the row's total: DPP butterflies (xor 1, xor 2 within quads, then the
+// half-row and row mirrors), VALU only.
+template <int CTRL>
+__device__ inline float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ inline float row16_sum(float v) {
+    v += dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_mov<0x141>(v);  // row_half_mirror
+    return v + dpp_mov<0x140>(v);  // row_mirror
+}
+
 __device__ inline float colgroup_max(float v) {
     uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
     lane_swap16(a, b);

@@ -485,6 +485,22 @@ int mha_check(const AtxMhaParams* p, const char* fn, MhaArgs& a, int& np, size_t
     a.y = p->y; a.ysb = p->y_stride_b; a.yss = (int)yss;
     a.L = L;
     a.c2 = p->scale * kLog2e;
+    // The attention half of a pre-LN block: the persistent form only.
+    if (p->ln_bias && !p->ln_weight) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: ln_bias without ln_weight", fn);
+    if (p->residual != 0 && p->residual != 1) ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: residual must be 0 or 1", fn);
+    if (p->ln_weight || p->residual) {
+        if (!(p->num_heads == 6 && E == 6 * kD && mha_ws_lds_bytes(E, L)))
+            ATX_FAIL(ATX_ERR_UNSUPPORTED, "%s: pre-LN / residual need 6 heads of 64 at 65..101 positions (got %d heads, embed_dim %d, seq %d)",
+                     fn, p->num_heads, E, L);
+        if (p->ln_weight && (!aligned16(p->ln_weight) || (p->ln_bias && !aligned16(p->ln_bias))))
+            ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: ln_weight / ln_bias must be 16-byte aligned [embed_dim]", fn);
+        if (p->ln_weight && !(p->ln_eps >= 0.f && p->ln_eps < __builtin_inff()))
+            ATX_FAIL(ATX_ERR_INVALID_ARGUMENT, "%s: ln_eps must be finite and >= 0 (got %g)", fn, (double)p->ln_eps);
+    }
+    a.ln_w = p->ln_weight;
+    a.ln_b = p->ln_bias;
+    a.ln_eps = p->ln_eps;
+    a.residual = p->residual;
     return ATX_OK;
 }
 
@@ -497,7 +513,8 @@ int mha_launch(const AtxMhaParams* p, const MhaArgs& a, int np, size_t lds, hipS
     // exists to compare them).
     if (const size_t wl = H == 6 && D == kD ? mha_ws_lds_bytes(p->embed_dim, p->seq) : 0) {
         const char* env = getenv("ATX_MHA_PERSISTENT");
-        if (!env || strcmp(env, "0") != 0) return mha_ws_launch(p->seq, p->causal != 0, bf, packed, p->batch, wl, st, a);
+        if (!env || strcmp(env, "0") != 0 || a.ln_w || a.residual)
+            return mha_ws_launch(p->seq, p->causal != 0, bf, packed, p->batch, wl, st, a);
     }
     if (packed) {
         if (bf) return p->causal ? dispatch_mha<__bf16, true, true>(H, D, np, p->batch, lds, st, a)

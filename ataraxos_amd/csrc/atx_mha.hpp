@@ -19,6 +19,10 @@ struct MhaArgs {
     int yss;
     int L;
     float c2;  // scale * log2(e)
+    const void* ln_w;  // pre-LN weight [E] (NULL: no LayerNorm)
+    const void* ln_b;  // pre-LN bias [E] (NULL: zero)
+    float ln_eps;
+    int residual;      // 1: y = x + layer output
 };
 
 namespace {

@@ -365,17 +365,52 @@ __device__ __forceinline__ void ws_store(const f32x4 (&acc)[3][NP], lds_t* sq, l
     }
 }
 
-// Y feature tiles ft0 .. ft0 + FT - 1 (+ bias) of sample b, rounded once; rows
-// past L are dropped.  In the MFMA layout a lane holds 4 consecutive features
-// (8 bytes) of one row per tile.  For each pair of tiles, two lane swaps
-// across the 16-lane groups (pairing groups 0,1 with 2,3, then 0 with 1 and 2
-// with 3) leave lane group g with features 8g .. 8g + 7 of the pair's 32, so
-// each store writes 16 bytes per lane and 64 contiguous bytes per row: half
-// the store instructions and write requests of 8-byte stores.
+// Residual rows of sample b for ws_store_y, loaded ahead of the
+// out-projection: per pair of tiles and position tile the 16 bytes of x a
+// lane's store covers after the lane swaps, and for an odd last tile its 8.
+template <int FT, int NP>
+struct WsRes {
+    u32x4 pair[FT / 2 > 0 ? FT / 2 : 1][NP];
+    u32x2 odd[NP];
+};
 template <typename T, int FT, int NP>
-__device__ __forceinline__ void ws_store_y(const f32x4 (&yacc)[FT][NP], const MhaArgs& a, int b, int ft0, int m, int g) {
+__device__ __forceinline__ void ws_load_res(WsRes<FT, NP>& r, const MhaArgs& a, int b, int ft0, int m, int g) {
+    const int L = a.L;
+    const rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + b * a.xsb, (uint32_t)(((L - 1) * a.xss + kWsE) * 2));
+#pragma unroll
+    for (int fp = 0; fp < FT / 2; ++fp)
+#pragma unroll
+        for (int q = 0; q < NP; ++q)
+            r.pair[fp][q] = buf_ld16_keep(rx, (uint32_t)((q * 16 + m) * a.xss + (ft0 + 2 * fp) * 16 + 8 * g) * 2);
+    if constexpr (FT % 2 == 1)
+#pragma unroll
+        for (int q = 0; q < NP; ++q)
+            r.odd[q] = __builtin_amdgcn_raw_buffer_load_b64(rx, (int)((q * 16 + m) * a.xss + (ft0 + FT - 1) * 16 + 4 * g) * 2, 0, 0);
+}
+
+// 16-bit pair w (as the layer rounded it) + residual pair r, rounded again:
+// x + attn(...) of transformer.py:143 in the 16-bit type.
+template <typename T>
+__device__ inline uint32_t add_res2(uint32_t w, uint32_t r) {
+    using M = Mfma16<T>;
+    return M::pack2(M::to_float((uint16_t)(w & 0xffffu)) + M::to_float((uint16_t)(r & 0xffffu)),
+                    M::to_float((uint16_t)(w >> 16)) + M::to_float((uint16_t)(r >> 16)));
+}
+
+// Y feature tiles ft0 .. ft0 + FT - 1 (+ bias) of sample b, rounded once (and,
+// with a residual, added to x and rounded again); rows past L are dropped.
+// In the MFMA layout a lane holds 4 consecutive features (8 bytes) of one row
+// per tile.  For each pair of tiles, two lane swaps across the 16-lane groups
+// (pairing groups 0,1 with 2,3, then 0 with 1 and 2 with 3) leave lane group
+// g with features 8g .. 8g + 7 of the pair's 32, so each store writes 16
+// bytes per lane and 64 contiguous bytes per row: half the store
+// instructions and write requests of 8-byte stores.
+template <typename T, int FT, int NP>
+__device__ __forceinline__ void ws_store_y(const f32x4 (&yacc)[FT][NP], const MhaArgs& a, int b, int ft0, int m, int g,
+                                           const WsRes<FT, NP>& res) {
     using M = Mfma16<T>;
     const int L = a.L;
+    const bool resid = a.residual != 0;
     const rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + b * a.ysb, (uint32_t)(((L - 1) * a.yss + kWsE) * 2));
     const T* const bo = static_cast<const T*>(a.bias[3]);
     // Bias of features 16 (ft0 + f) + 4g .. + 3, read before any store (a
@@ -402,15 +437,22 @@ __device__ __forceinline__ void ws_store_y(const f32x4 (&yacc)[FT][NP], const Mh
             lane_swap32(x1, y1);
             lane_swap16(x0, y0);
             lane_swap16(x1, y1);
-            buf_st16_cached(ry, (uint32_t)((q * 16 + m) * a.yss + (ft0 + 2 * fp) * 16 + 8 * g) * 2, u32x4{x0, x1, y0, y1});
+            u32x4 out = u32x4{x0, x1, y0, y1};
+            if (resid)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) out[i] = add_res2<T>(out[i], res.pair[fp][q][i]);
+            buf_st16_cached(ry, (uint32_t)((q * 16 + m) * a.yss + (ft0 + 2 * fp) * 16 + 8 * g) * 2, out);
         }
     if constexpr (FT % 2 == 1)  // an odd last tile: 8 bytes per lane
 #pragma unroll
         for (int q = 0; q < NP; ++q) {
             const f32x4& y = yacc[FT - 1][q];
             const f32x4& bb = bv[FT - 1];
-            buf_st8_cached(ry, (uint32_t)((q * 16 + m) * a.yss + (ft0 + FT - 1) * 16 + 4 * g) * 2,
-                           u32x2{M::pack2(y[0] + bb[0], y[1] + bb[1]), M::pack2(y[2] + bb[2], y[3] + bb[3])});
+            u32x2 out = u32x2{M::pack2(y[0] + bb[0], y[1] + bb[1]), M::pack2(y[2] + bb[2], y[3] + bb[3])};
+            if (resid)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) out[i] = add_res2<T>(out[i], res.odd[q][i]);
+            buf_st8_cached(ry, (uint32_t)((q * 16 + m) * a.yss + (ft0 + FT - 1) * 16 + 4 * g) * 2, out);
         }
 }
 
@@ -444,11 +486,12 @@ __device__ __forceinline__ void ws_load_x(lds_t* sx, const MhaArgs& a, int b, in
     }
 }
 
-// The next sample's X rows in two halves for the producers (256 threads):
-// the loads go out right after the last head's projection MFMAs, into
-// registers, and land in LDS a step later, once every producer is done reading
-// the current X.  kWsXU loads per thread cover the longest sequence the kernel
-// takes (kWsMaxL rows).
+// The next sample's X rows in two halves for the producers: the loads go out
+// right after the last head's projection MFMAs, into registers, and land in
+// LDS a step later, once every producer is done reading the current X.
+// Producer p takes rows p, p + 4, p + 8, ... (whole rows, so that it can
+// normalise them itself right after writing them); kWsXU loads per lane
+// cover the longest sequence the kernel takes (kWsMaxL rows).
 constexpr int kWsMaxL = 101;
 #ifndef ATX_MHA_WS_XEARLY
 #define ATX_MHA_WS_XEARLY 8
@@ -456,35 +499,100 @@ constexpr int kWsMaxL = 101;
 constexpr int kWsXEarly = ATX_MHA_WS_XEARLY;  // loads issued before the last head's store
 template <int NP>
 constexpr int ws_xu() {
-    return ((16 * NP < kWsMaxL ? 16 * NP : kWsMaxL) * (kWsE / 8) + 255) / 256;
+    return (((16 * NP < kWsMaxL ? 16 * NP : kWsMaxL) + 3) / 4 * (kWsE / 8) + 63) / 64;
 }
 template <typename T, int UX, int U0, int U1>
-__device__ __forceinline__ void ws_x_issue(u32x4 (&v)[UX], const MhaArgs& a, int b, int t) {
+__device__ __forceinline__ void ws_x_issue(u32x4 (&v)[UX], const MhaArgs& a, int b, int p, int lane) {
     constexpr int XC = kWsE / 8;
     const int L = opaque_s(a.L);
-    t = opaque_v(t);
-    const int N = L * XC;
+    lane = opaque_v(lane);
     const rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + b * a.xsb, (uint32_t)(((L - 1) * a.xss + kWsE) * 2));
     // No branches (a load past the rows reads zero): registers defined on
     // every path stay in registers across the code between issue and commit.
 #pragma unroll
     for (int u = U0; u < U1; ++u) {
-        const int idx = u * 256 + t;
-        const int r = idx / XC, c = idx - (idx / XC) * XC;
-        v[u] = buf_ld16(rx, idx < N ? (uint32_t)(r * a.xss + c * 8) * 2 : 0xfffffff0u);
+        const int j = u * 64 + lane;
+        const int r = p + 4 * (j / XC), c = j - (j / XC) * XC;
+        v[u] = buf_ld16(rx, r < L ? (uint32_t)(r * a.xss + c * 8) * 2 : 0xfffffff0u);
     }
 }
 template <int UX>
-__device__ __forceinline__ void ws_x_commit(const u32x4 (&v)[UX], lds_t* sx, int L, int t) {
+__device__ __forceinline__ void ws_x_commit(const u32x4 (&v)[UX], lds_t* sx, int L, int p, int lane) {
     constexpr int XC = kWsE / 8;
     L = opaque_s(L);
-    t = opaque_v(t);
-    const int N = L * XC;
+    lane = opaque_v(lane);
 #pragma unroll
     for (int u = 0; u < UX; ++u) {
-        const int idx = u * 256 + t;
-        const int r = idx / XC, c = idx - (idx / XC) * XC;
-        if (idx < N) lds_st16(sx + eoff<kWsE>(r, c), v[u]);
+        const int j = u * 64 + lane;
+        const int r = p + 4 * (j / XC), c = j - (j / XC) * XC;
+        if (r < L) lds_st16(sx + eoff<kWsE>(r, c), v[u]);
+    }
+}
+
+// Pre-LN of transformer.py:143 (nn.LayerNorm(embed_dim)) on X rows r0,
+// r0 + rstep, ... below L, in place in LDS, by one wave: per row the fp32
+// mean and biased variance over the E elements, (x - mean) * rsqrt(var +
+// eps) * weight + bias, rounded to T.  Four rows per pass: lanes 16k .. 16k +
+// 15 hold row r0 + rstep (4 pass + k), lane i its 16-byte chunks i, i + 16,
+// i + 32; row sums over the 16 lanes by DPP butterflies.
+template <typename T>
+__device__ __forceinline__ void ws_layernorm_rows(lds_t* sx, const MhaArgs& a, int r0, int rstep, int lane) {
+    using M = Mfma16<T>;
+    constexpr int XC = kWsE / 8;
+    constexpr int CPL = XC / 16;  // chunks per lane
+    const int L = opaque_s(a.L);
+    lane = opaque_v(lane);
+    const int k = lane >> 4, i = lane & 15;
+    const rsrc_t rg = make_rsrc(a.ln_w, kWsE * 2), rb = make_rsrc(a.ln_b, a.ln_b ? kWsE * 2 : 0);
+    u32x4 gw[CPL], gb[CPL];  // this lane's columns of weight and bias (a NULL bias reads zeros)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        gw[j] = buf_ld16_keep(rg, (uint32_t)(i + 16 * j) * 16);
+        gb[j] = buf_ld16_keep(rb, (uint32_t)(i + 16 * j) * 16);
+    }
+    const auto lo = [](uint32_t w) { return M::to_float((uint16_t)(w & 0xffffu)); };
+    const auto hi = [](uint32_t w) { return M::to_float((uint16_t)(w >> 16)); };
+    const float inv_e = 1.f / (float)kWsE;
+    for (int base = r0; base < L; base += 4 * rstep) {
+        const int r = base + rstep * k;
+        const bool ok = r < L;
+        float xv[CPL][8];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const u32x4 c = ok ? lds_ld16(sx + eoff<kWsE>(r, i + 16 * j)) : u32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                xv[j][2 * w] = lo(c[w]);
+                xv[j][2 * w + 1] = hi(c[w]);
+            }
+        }
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += xv[j][e];
+        sum = row16_sum(sum);
+        const float mean = sum * inv_e;
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                xv[j][e] -= mean;
+                ss = __builtin_fmaf(xv[j][e], xv[j][e], ss);
+            }
+        ss = row16_sum(ss);
+        const float rstd = __builtin_amdgcn_rsqf(ss * inv_e + a.ln_eps);
+        if (ok)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                u32x4 c;
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    c[w] = M::pack2(__builtin_fmaf(xv[j][2 * w] * rstd, lo(gw[j][w]), lo(gb[j][w])),
+                                    __builtin_fmaf(xv[j][2 * w + 1] * rstd, hi(gw[j][w]), hi(gb[j][w])));
+                lds_st16(sx + eoff<kWsE>(r, i + 16 * j), c);
+            }
     }
 }
 
@@ -516,9 +624,11 @@ __device__ __forceinline__ void ws_out_proj(f32x4 (&yacc)[FT][NP], const u32x4 (
                                             int b, int s, int ft0, int m, int g) {
     if (s >= 2 || (s == 0 && b != (int)blockIdx.x)) {
         const int hh = s >= 2 ? s - 2 : kWsH - 1;
+        WsRes<FT, NP> res;  // the previous sample's residual rows, in flight during the out-projection
+        if (s == 0 && a.residual) ws_load_res<T, FT, NP>(res, a, b - (int)gridDim.x, ft0, m, g);
         out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + (hh & 1) * c.slot, m, g);
         if (s == 0) {
-            ws_store_y<T, FT, NP>(yacc, a, b - (int)gridDim.x, ft0, m, g);
+            ws_store_y<T, FT, NP>(yacc, a, b - (int)gridDim.x, ft0, m, g, res);
 #pragma unroll
             for (int f = 0; f < FT; ++f)
 #pragma unroll
@@ -577,23 +687,31 @@ __device__ __forceinline__ void ws_producer(const WsCtx& c, const MhaArgs& a, co
             project(b, kWsH - 1, m, g, acc);
             // (Part of the loads here; the rest once acc is stored.)
             __builtin_amdgcn_sched_barrier(0);
-            ws_x_issue<T, ws_xu<NP>(), 0, kWsXEarly>(xv, a, more ? b + grid : b, p * 64 + ln);
+            ws_x_issue<T, ws_xu<NP>(), 0, kWsXEarly>(xv, a, more ? b + grid : b, p, ln);
             __syncthreads();
             store(kWsH - 1, m, g, acc);
             __syncthreads();
         }
         __builtin_amdgcn_sched_barrier(0);
-        ws_x_issue<T, ws_xu<NP>(), kWsXEarly, ws_xu<NP>()>(xv, a, more ? b + grid : b, p * 64 + ln);
+        ws_x_issue<T, ws_xu<NP>(), kWsXEarly, ws_xu<NP>()>(xv, a, more ? b + grid : b, p, ln);
         __builtin_amdgcn_sched_barrier(0);
         ws_out_proj<T, FT, NP>(yacc, wo, c, a, b, kWsH, ft0, m, g);
-        if (more) ws_x_commit<ws_xu<NP>()>(xv, lds_opaque(c.sx0), a.L, p * 64 + ln);
+        if (more) {
+            ws_x_commit<ws_xu<NP>()>(xv, lds_opaque(c.sx0), a.L, p, ln);
+            if (a.ln_w) {
+                wave_lds_handoff();  // the wave reads back the rows it wrote
+                ws_layernorm_rows<T>(lds_opaque(c.sx0), a, p, 4, c.lane);
+            }
+        }
         ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, kWsH - 1);
         __syncthreads();
     }
     const int m = c.lane & 15, g = c.lane >> 4;
     const int last = blockIdx.x + ((c.batch - 1 - (int)blockIdx.x) / grid) * grid;
+    WsRes<FT, NP> res;
+    if (a.residual) ws_load_res<T, FT, NP>(res, a, last, ft0, m, g);
     out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + ((kWsH - 1) & 1) * c.slot, m, g);
-    ws_store_y<T, FT, NP>(yacc, a, last, ft0, m, g);
+    ws_store_y<T, FT, NP>(yacc, a, last, ft0, m, g, res);
 }
 
 // Consumer wave 4 + cq (cq 0..3): query tiles cq and cq + 4; owns the kWsFTC
@@ -649,8 +767,10 @@ __device__ __forceinline__ void ws_consumer(const WsCtx& c, const MhaArgs& a, co
     }
     const int m = c.lane & 15, g = c.lane >> 4;
     const int last = blockIdx.x + ((c.batch - 1 - (int)blockIdx.x) / grid) * grid;
+    WsRes<FT, NP> res;
+    if (a.residual) ws_load_res<T, FT, NP>(res, a, last, ft0, m, g);
     out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + ((kWsH - 1) & 1) * c.slot, m, g);
-    ws_store_y<T, FT, NP>(yacc, a, last, ft0, m, g);
+    ws_store_y<T, FT, NP>(yacc, a, last, ft0, m, g, res);
 }
 
 template <typename T, int NP, bool CAUSAL, bool PK>
@@ -682,6 +802,10 @@ __global__ __launch_bounds__(kThreads) void mha_ws(MhaArgs a, int batch) {
         lds_st16(c.ss0 + s * c.slot + 2 * c.LQ * kD * 2 + LP * kD * 2 + j * 16, u32x4{0, 0, 0, 0});
     }
     __syncthreads();
+    if (a.ln_w) {  // (uniform: the same for every wave)
+        ws_layernorm_rows<T>(c.sx0, a, wave, kWaves, c.lane);
+        __syncthreads();
+    }
 
     // The two roles run separate loops with the same barriers in the same
     // order (the branch is uniform over each wave), each with its own

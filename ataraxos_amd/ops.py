@@ -486,6 +486,13 @@ def mha_forward_supported(embed_dim: int, num_heads: int, seq: int, dtype: torch
     )
 
 
+def mha_block_supported(embed_dim: int, num_heads: int, seq: int, dtype: torch.dtype) -> bool:
+    """True when :func:`mha_forward` also takes the pre-LN and the residual of
+    a pre-LN block (the persistent kernel's shape): bf16/fp16, 6 heads of 64,
+    65 to 101 positions -- the Move network layer of BASELINE config 3."""
+    return dtype in _BWD_DTYPES and num_heads == 6 and embed_dim == 384 and 65 <= seq <= 101
+
+
 def mha_forward(
     x: torch.Tensor,
     w_q: torch.Tensor,
@@ -504,6 +511,10 @@ def mha_forward(
     repack: bool = False,
     workspace: torch.Tensor | None = None,
     noalloc: bool = False,
+    ln_weight: torch.Tensor | None = None,
+    ln_bias: torch.Tensor | None = None,
+    ln_eps: float = 1e-5,
+    residual: bool = False,
 ) -> torch.Tensor:
     """Whole self-attention layer in one launch (no autograd):
     ``out_proj(attention(q_proj(x), k_proj(x), v_proj(x)))`` with the
@@ -523,7 +534,14 @@ def mha_forward(
       What the modules use: no cached copy can go stale;
     * ``noalloc=True``: as ``repack``, with the library's own per-GPU array in
       place of the workspace (``atx_mha_fwd_noalloc``: the C call allocates
-      nothing; embed_dim <= 512; calls that overlap on one GPU race)."""
+      nothing; embed_dim <= 512; calls that overlap on one GPU race).
+
+    The attention half of a pre-LN block, ``x + layer(LayerNorm(x))``
+    (stratego/networks/transformer.py:143, dropout inactive), in the same
+    launch: ``ln_weight`` / ``ln_bias`` / ``ln_eps`` (an ``nn.LayerNorm``'s
+    parameters) normalise each row first, ``residual=True`` adds x to the
+    layer output (rounded, then rounded again after the add).  Shapes of
+    :func:`mha_block_supported` only; ``out`` may be x."""
     _require_device("mha_forward", x, w_q, w_k, w_v, w_o)
     if x.dim() != 3:
         raise ValueError("mha_forward: x must be [batch, seq, embed_dim]")
@@ -545,6 +563,26 @@ def mha_forward(
         biases.append(t)
     if packed + repack + noalloc > 1:
         raise ValueError("mha_forward: packed, repack and noalloc are exclusive")
+    ln = []
+    if ln_bias is not None and ln_weight is None:
+        raise ValueError("mha_forward: ln_bias without ln_weight")
+    if ln_weight is not None or residual:
+        if not mha_block_supported(e, num_heads, l, x.dtype):
+            raise NotImplementedError(
+                f"mha_forward: pre-LN / residual need 6 heads of 64 at 65..101 positions (got {num_heads} heads, "
+                f"embed_dim {e}, seq {l})"
+            )
+        for name, t in (("ln_weight", ln_weight), ("ln_bias", ln_bias)):
+            if t is not None:
+                if tuple(t.shape) != (e,) or t.dtype != x.dtype:
+                    raise ValueError(f"mha_forward: {name} must be [{e}] in {x.dtype}")
+                _require_device("mha_forward", x, t)
+                t = _aligned_rows(t.contiguous())
+            ln.append(t)
+        if not (ln_eps >= 0.0 and math.isfinite(ln_eps)):
+            raise ValueError(f"mha_forward: ln_eps must be finite and >= 0 (got {ln_eps})")
+    else:
+        ln = [None, None]
     x = _aligned_rows(x)
     ws = [_aligned_rows(w) if w.is_contiguous() else _aligned_rows(w.contiguous()) for w in (w_q, w_k, w_v, w_o)]
     if out is None:
@@ -564,6 +602,9 @@ def mha_forward(
     p.b_q, p.b_k, p.b_v, p.b_o = (t.data_ptr() if t is not None else None for t in biases)
     p.y, p.y_stride_b, p.y_stride_s = out.data_ptr(), out.stride(0), out.stride(1)
     p.scale = float(scale)
+    p.ln_weight, p.ln_bias = (t.data_ptr() if t is not None else None for t in ln)
+    p.ln_eps = float(ln_eps)
+    p.residual = 1 if residual else 0
     if repack:
         need = mha_workspace_bytes(e)
         if workspace is None:

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ATX_ABI_VERSION 1
+#define ATX_ABI_VERSION 2
 
 /* Return codes. */
 #define ATX_OK 0
@@ -287,6 +287,18 @@ typedef struct AtxMhaParams {
     void* y;
     int64_t y_stride_b, y_stride_s;
     float scale; /* the reference uses 1 / sqrt(head_dim) */
+    /* The attention half of a pre-LN block, y = x + layer(LayerNorm(x))
+     * (stratego/networks/transformer.py:143 with dropout inactive): with
+     * ln_weight set, each x row is normalised (fp32 mean and biased
+     * variance, eps ln_eps, then * ln_weight + ln_bias, rounded to dtype)
+     * before the projections; with residual = 1 the layer output, rounded to
+     * dtype, is added to x and rounded again.  y may be x itself.  Both
+     * need the persistent form's shape (6 heads of 64, 65 <= seq <= 101);
+     * elsewhere they are refused with ATX_ERR_UNSUPPORTED.  NULL / 0: off. */
+    const void* ln_weight; /* [embed_dim], dtype; NULL: no LayerNorm */
+    const void* ln_bias;   /* [embed_dim], dtype; NULL: zero */
+    float ln_eps;
+    int32_t residual;
 } AtxMhaParams;
 
 /*

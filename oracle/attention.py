@@ -157,3 +157,35 @@ def mha_forward(
     v = linear(src, weights["v_proj.weight"], weights.get("v_proj.bias")).reshape(b, s_kv, kv_heads, d)
     o = attention(q, k, v, causal=causal and key_value is None)
     return linear(o.reshape(b, s_q, num_heads * d), weights["out_proj.weight"], weights.get("out_proj.bias"))
+
+
+def layer_norm(x: np.ndarray, weight: np.ndarray | None, bias: np.ndarray | None, eps: float = 1e-5) -> np.ndarray:
+    """``nn.LayerNorm`` over the last axis in float64: ``(x - mean) /
+    sqrt(var + eps) * weight + bias`` with the biased variance, as torch's
+    layer_norm defines it (the ``ln1`` / ``ln2`` of
+    stratego/networks/transformer.py:116-118)."""
+    mean = x.mean(axis=-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=-1, keepdims=True)
+    y = (x - mean) / np.sqrt(var + eps)
+    if weight is not None:
+        y = y * weight
+    if bias is not None:
+        y = y + bias
+    return y
+
+
+def preln_attention_half(
+    x: np.ndarray,
+    weights: dict[str, np.ndarray],
+    num_heads: int,
+    causal: bool = False,
+    eps: float = 1e-5,
+) -> np.ndarray:
+    """The attention half of ``PreLNTransformerBlock.forward``
+    (stratego/networks/transformer.py:143 with dropout inactive):
+    ``x + attn(ln1(x))``.  ``weights`` holds the block's state_dict entries
+    ``ln1.weight``, ``ln1.bias`` and ``attn.{q,k,v,out}_proj.weight`` (and
+    optional ``.bias``)."""
+    h = layer_norm(x, weights.get("ln1.weight"), weights.get("ln1.bias"), eps)
+    attn_w = {k[len("attn."):]: v for k, v in weights.items() if k.startswith("attn.")}
+    return x + mha_forward(h, None, attn_w, num_heads, causal=causal)

@@ -283,6 +283,41 @@ def test_fused_layer_validation_codes():
     _expect("atx_mha_fwd_packed", p, _lib.ERR_UNSUPPORTED, "LDS")
 
 
+def test_preln_block_validation_codes():
+    """The pre-LN / residual fields of AtxMhaParams are checked before any HIP
+    call: a bias without a weight, a residual flag other than 0/1, a negative
+    or non-finite eps, misaligned LayerNorm vectors, and any shape outside
+    the persistent kernel's (6 heads of 64 at 65..101 positions)."""
+    p = _lib.MhaParams()
+    p.abi_version, p.dtype, p.batch, p.seq, p.embed_dim, p.num_heads = _lib.ABI_VERSION, _lib.DTYPE_BF16, 4, 100, 384, 6
+    p.x = p.w_q = p.w_k = p.w_v = p.w_o = p.y = 1 << 20  # never dereferenced: every case fails validation
+    p.x_stride_b = p.y_stride_b = 100 * 384
+    p.x_stride_s = p.y_stride_s = 384
+    p.scale = 0.125
+    p.ln_eps = 1e-5
+    cases = [
+        (dict(ln_bias=1 << 21), _lib.ERR_INVALID_ARGUMENT, "ln_bias without ln_weight"),
+        (dict(residual=2), _lib.ERR_INVALID_ARGUMENT, "residual"),
+        (dict(ln_weight=(1 << 21) + 2), _lib.ERR_INVALID_ARGUMENT, "16-byte"),
+        (dict(ln_weight=1 << 21, ln_bias=(1 << 22) + 8), _lib.ERR_INVALID_ARGUMENT, "16-byte"),
+        (dict(ln_weight=1 << 21, ln_eps=-1.0), _lib.ERR_INVALID_ARGUMENT, "ln_eps"),
+        (dict(ln_weight=1 << 21, ln_eps=float("inf")), _lib.ERR_INVALID_ARGUMENT, "ln_eps"),
+        (dict(residual=1, seq=64), _lib.ERR_UNSUPPORTED, "pre-LN / residual"),
+        (dict(residual=1, seq=102), _lib.ERR_UNSUPPORTED, "pre-LN / residual"),
+        (dict(ln_weight=1 << 21, num_heads=8), _lib.ERR_UNSUPPORTED, "pre-LN / residual"),
+        (dict(residual=1, embed_dim=512, num_heads=8, x_stride_s=512, y_stride_s=512), _lib.ERR_UNSUPPORTED,
+         "pre-LN / residual"),
+    ]
+    for fields, code, text in cases:
+        saved = {k: getattr(p, k) for k in fields}
+        for k, v in fields.items():
+            setattr(p, k, v)
+        for name in ("atx_mha_fwd", "atx_mha_fwd_packed"):
+            _expect(name, p, code, text)
+        for k, v in saved.items():
+            setattr(p, k, v)
+
+
 def test_workspace_entry_point_validation_codes():
     """atx_mha_fwd_ws validates the layer as atx_mha_fwd does, then the
     workspace (size, alignment, overlap), all before any HIP call."""
