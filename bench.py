@@ -21,7 +21,10 @@ roofline = 18.2 M samples/s).  Also reported on the same line:
 * ``e2e``: the full MultiHeadAttention forward of the 8 layers plus the
   residual, as the module runs it in inference (one launch of the fused layer
   kernel per layer), with its MFMA rate (B x 133.3 MFLOP per layer), and the
-  same with the unfused path (hipBLASLt projections + attention kernel);
+  same with the unfused path (hipBLASLt projections + attention kernel); the
+  chain with the residual inside the layer kernel; the attention halves of 8
+  pre-LN blocks (LayerNorm + layer + residual, one launch each); one layer of
+  the reference Move network's 8 x 48 at L=101;
 * ``kq_policy``: the fused key-query policy kernel at config C2;
 * ``belief_attention``: the attention kernel at the config C4 shapes
   (encoder self, decoder causal self, decoder cross with key padding);
@@ -220,6 +223,44 @@ def time_e2e(torch, batch, seq, embed, heads, layers_n, steps, warmup, dev, fuse
         x = x0
         for m in mods:
             x = x + m(x)
+        return x
+
+    with torch.inference_mode():
+        for _ in range(warmup):
+            step()
+        _settle(torch, step)
+        a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            step()
+        z.record()
+        torch.cuda.synchronize()
+    return a.elapsed_time(z) / steps
+
+
+def time_chain(torch, ops, batch, seq, embed, heads, layers_n, steps, warmup, dev, ln=False, fuse=True):
+    """The C3 chain with the residual inside the layer kernel: per layer one
+    launch rearranging the weights and one launch computing x + MHA(x) (with
+    ``ln``: x + MHA(LayerNorm(x)), the attention half of the reference's
+    pre-LN block, transformer.py:143).  Without ``fuse`` the same chain as
+    separate launches: LayerNorm (torch), the fused layer, the add."""
+    g = torch.Generator(device=dev).manual_seed(47)
+    x0 = torch.randn(batch, seq, embed, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    ws = [[(torch.randn(embed, embed, generator=g, device=dev) * 0.02).to(torch.bfloat16) for _ in range(4)]
+          for _ in range(layers_n)]
+    lns = [((1 + 0.1 * torch.randn(embed, generator=g, device=dev)).to(torch.bfloat16),
+            (0.1 * torch.randn(embed, generator=g, device=dev)).to(torch.bfloat16)) for _ in range(layers_n)]
+    work = torch.empty(ops.mha_workspace_bytes(embed), dtype=torch.uint8, device=dev)
+
+    def step():
+        x = x0
+        for w, (lw, lb) in zip(ws, lns):
+            if fuse:
+                kw = dict(ln_weight=lw, ln_bias=lb) if ln else {}
+                x = ops.mha_forward(x, *w, num_heads=heads, repack=True, workspace=work, residual=True, **kw)
+            else:
+                h = torch.nn.functional.layer_norm(x, (embed,), lw, lb, 1e-5) if ln else x
+                x = x + ops.mha_forward(h, *w, num_heads=heads, repack=True, workspace=work)
         return x
 
     with torch.inference_mode():
@@ -674,6 +715,41 @@ def main() -> int:
             "samples_per_s": batch / (layer_ms * 1e-3),
             "mfma_tflops": layer_flops / (layer_ms * 1e-3) / 1e12,
             "mfma_frac": layer_flops / (layer_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+        }
+        reps = max(5, args.steps // 5)
+        chain_ms = time_chain(torch, ops, batch, seq, embed, heads, args.layers, reps, 3, dev)
+        result["e2e"]["residual_in_kernel"] = {
+            "what": "the same 8-layer chain x <- x + MHA(x) with the residual added inside the fused layer "
+                    "(per layer: one weight-rearranging launch, one launch of atx_mha_fwd_ws with residual=1)",
+            "ms_per_step": chain_ms,
+            "samples_per_s": batch / (chain_ms * 1e-3),
+            "mfma_frac": args.layers * layer_flops / (chain_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+            "per_layer_us": chain_ms * 1e3 / args.layers,
+        }
+        pre_ms = time_chain(torch, ops, batch, seq, embed, heads, args.layers, reps, 3, dev, ln=True)
+        pre_unf_ms = time_chain(torch, ops, batch, seq, embed, heads, args.layers, reps, 3, dev, ln=True, fuse=False)
+        result["e2e"]["preln_block_half"] = {
+            "what": "8 pre-LN block attention halves x <- x + MHA(LayerNorm(x)) (transformer.py:143), each one "
+                    "launch (LayerNorm, projections, attention, output projection, residual) after the weight "
+                    "rearrangement; unfused: torch LayerNorm, the fused layer, a separate add",
+            "ms_per_step": pre_ms,
+            "per_layer_us": pre_ms * 1e3 / args.layers,
+            "mfma_frac": args.layers * layer_flops / (pre_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+            "unfused_ms_per_step": pre_unf_ms,
+        }
+        # The reference Move network's own layer: 8 heads x 48 at 101 positions.
+        gm = torch.Generator(device=dev).manual_seed(48)
+        xm = torch.randn(batch, 101, embed, generator=gm, device=dev).to(torch.bfloat16)
+        wm = [ops.mha_pack_weight((torch.randn(embed, embed, generator=gm, device=dev) * 0.02).to(torch.bfloat16)) for _ in range(4)]
+        ym = torch.empty_like(xm)
+        move_ms = _mean_launch_ms(torch, lambda: ops.mha_forward(xm, *wm, num_heads=8, out=ym, packed=True), args.steps, args.warmup)
+        move_flops = batch * (4 * 2 * 101 * embed * embed + 8 * 2 * 2 * 101 * 101 * 48)
+        result["e2e"]["fused_layer_move_ref_8x48"] = {
+            "what": "one layer of the reference Move network's own shape (B=4096, L=101, 8 heads x 48) "
+                    "through atx_mha_fwd_packed",
+            "kernel_us": move_ms * 1e3,
+            "samples_per_s": batch / (move_ms * 1e-3),
+            "mfma_frac": move_flops / (move_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
         }
         result["kq_policy"] = time_kq(torch, ops, batch, dev, args.steps, args.warmup)
         result["belief_attention"] = time_belief(torch, ops, dev, args.steps, args.warmup)
