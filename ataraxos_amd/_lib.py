@@ -14,7 +14,7 @@ import os
 import threading
 from pathlib import Path
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK = 0
 ERR_INVALID_ARGUMENT = -1
@@ -33,6 +33,7 @@ LIB_NAME = "libataraxos_attn.so"
 
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
+_u64 = ctypes.c_uint64
 _ptr = ctypes.c_void_p
 _f32 = ctypes.c_float
 
@@ -67,6 +68,10 @@ class AttnParams(ctypes.Structure):
         ("causal", _i32),
         ("key_pad", _ptr),
         ("key_pad_stride_b", _i64),
+        ("dropout_p", _f32),
+        ("reserved_dropout", _i32),
+        ("dropout_seed", _u64),
+        ("dropout_offset", _u64),
     ]
 
 
@@ -218,6 +223,10 @@ class AttnBwdParams(ctypes.Structure):
         ("causal", _i32),
         ("key_pad", _ptr),
         ("key_pad_stride_b", _i64),
+        ("dropout_p", _f32),
+        ("reserved_dropout", _i32),
+        ("dropout_seed", _u64),
+        ("dropout_offset", _u64),
     ]
 
 
@@ -253,6 +262,7 @@ ENTRY_POINTS = {
     "atx_mha_fwd_ws": (ctypes.c_int, [ctypes.POINTER(MhaParams), _ptr, _i64, _ptr]),
     "atx_mha_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(MhaParams), _ptr]),
     "atx_attn_decode_fwd": (ctypes.c_int, [ctypes.POINTER(DecodeParams), _ptr]),
+    "atx_dropout_mask": (ctypes.c_int, [_i32, _i32, _i32, _i32, _f32, _u64, _u64, _ptr, _ptr]),
     # include/ataraxos_rollout.h
     "atx_rollout_apply": (ctypes.c_int, [_state_ptr, _ptr, _ptr]),
     "atx_rollout_legal_mask": (ctypes.c_int, [_state_ptr, _ptr, _ptr]),

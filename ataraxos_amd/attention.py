@@ -25,10 +25,14 @@ Backends (``backend`` property, the slot of attention.py:122-146):
   launch on every call) where that is faster, i.e. from the sequence length
   :data:`FUSED_MIN_SEQ` (:data:`FUSED_MIN_SEQ_D48`) gives for the head count;
   with autograd the projections stay ``nn.Linear`` and the attention
-  kernel's backward applies.
-* ``"math"`` — tensors on the CPU, or training with ``dropout > 0`` (the
-  kernel has no dropout, as the reference's FA3 backend has none:
-  attention.py:134-138).  It keeps the semantics of attention.py:281-316.
+  kernel's backward applies.  Training with ``dropout > 0`` at head_dim 64
+  or 48 runs the kernels' own attention dropout (``ops.attention`` with
+  ``dropout_p``: each weight dropped by a hash of its index under a seed
+  drawn from torch's default generator per call; the backward recomputes the
+  same decisions).
+* ``"math"`` — tensors on the CPU, or training with ``dropout > 0`` at
+  other head sizes (attention.py:134-138 likewise routes dropout away from
+  its FA3 backend).  It keeps the semantics of attention.py:281-316.
 """
 
 from __future__ import annotations
@@ -131,11 +135,12 @@ class MultiHeadAttention(nn.Module):
 
     @property
     def backend(self) -> str:
-        """``"hip"`` on a GPU, ``"math"`` on the CPU or when dropout must run."""
+        """``"hip"`` on a GPU, ``"math"`` on the CPU or when dropout must run
+        at a head size the kernels have no dropout for."""
         device = next(self.parameters()).device
         if device.type != "cuda":
             return "math"
-        if self.training and self.dropout > 0.0:
+        if self.training and self.dropout > 0.0 and self.head_dim not in ops.DROPOUT_HEAD_DIMS:
             return "math"
         return "hip"
 
@@ -163,6 +168,8 @@ class MultiHeadAttention(nn.Module):
         a shape the fused kernel covers, and a sequence long enough for it to
         beat the unfused path (:data:`FUSED_MIN_SEQ`)."""
         if not self.fuse_layer or self.backend != "hip" or self.num_kv_heads != self.num_heads:
+            return False
+        if self.training and self.dropout > 0.0:
             return False
         if self.head_dim not in (48, 64):
             return False
@@ -202,7 +209,8 @@ class MultiHeadAttention(nn.Module):
                 f"MultiHeadAttention: the HIP kernel does not cover head_dim={self.head_dim}, "
                 f"seq_kv={k.shape[1]}, dtype={q.dtype} (head_dim in {ops.HEAD_DIMS}, seq_kv <= {ops.MAX_SEQ_KV})"
             )
-        return ops.attention(q, k, v, causal=is_causal)
+        p = self.dropout if (self.training and self.dropout > 0.0) else 0.0
+        return ops.attention(q, k, v, causal=is_causal, dropout_p=p)
 
     def _forward_math(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, is_causal: bool) -> torch.Tensor:
         p = self.dropout if (self.training and self.dropout > 0.0) else 0.0

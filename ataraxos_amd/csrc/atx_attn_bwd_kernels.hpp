@@ -26,6 +26,7 @@ struct BwdArgs {
     int QB;             // LOOP variants: query rows staged per block (multiple of 32; fp32: 16)
     float c2, scale;  // c2 = scale * log2(e)
     int causal;
+    DropKey drop;  // attention dropout (the DROP instantiations only)
 };
 
 namespace {
@@ -83,7 +84,13 @@ constexpr int bwd_occ() {
 // store -- the sum over the repeat_interleave'd heads of attention.py:210-220
 // and over all queries, without atomics.  dQ rows are complete per block
 // (every key is resident).
-template <typename T, int D, int NKC, bool LOOP>
+//
+// DROP (attention dropout, LOOP variants only): the forward used P' = P o M,
+// M = keep / (1 - p) from drop_hash.  dV = P'^T dO, and with dP' = dO V^T,
+// dS = P o (M o dP' - delta); delta = rowsum(P o M o dP') = rowsum(O o dO)
+// with O the forward's dropout output, so delta is unchanged.  The dP'
+// accumulators then start at 0 and M joins before -delta.
+template <typename T, int D, int NKC, bool LOOP, bool DROP = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(bwd_occ<D, NKC, LOOP>(), 8)))
 void attn_bwd_16bit(BwdArgs a) {
     using M = Mfma16<T>;
@@ -358,6 +365,8 @@ void attn_bwd_16bit(BwdArgs a) {
                 lds_st4(sdelta + qrow * 4, __builtin_bit_cast(uint32_t, ndelta));
             }
             const f32x4 ndelta4 = f32x4{ndelta, ndelta, ndelta, ndelta};
+            // dropout row of this query: element index of key 0
+            const uint64_t drow = DROP ? (uint64_t)(((int64_t)b * a.H + h) * a.Sq + qabs) * (uint64_t)a.Skv : 0;
             // dP^T - delta = V dO^T - delta (the accumulator starts at -delta),
             // scale * dS^T = P^T (dP^T - delta) * scale, packed per 32-key chunk
             u32x4 dsk[NKC];
@@ -368,9 +377,16 @@ void attn_bwd_16bit(BwdArgs a) {
                 for (int hh = 0; hh < 2; ++hh) {
                     const int kt = 2 * c + hh;
                     if (kt * 16 < kend) {
-                        f32x4 dp = M::mma(ld_op(sv + kt * 16 * RS, 0), doop[0], ndelta4);
+                        f32x4 dp = M::mma(ld_op(sv + kt * 16 * RS, 0), doop[0], DROP ? f32x4{0.f, 0.f, 0.f, 0.f} : ndelta4);
 #pragma unroll
                         for (int i = 1; i < NI; ++i) dp = M::mma(ld_op(sv + kt * 16 * RS, i), doop[i], dp);
+                        if constexpr (DROP) {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const bool keep = drop_hash(drow + (uint64_t)(kt * 16 + 4 * g + i), a.drop.k0, a.drop.k1) >= a.drop.thresh;
+                                dp[i] = __builtin_fmaf(dp[i], keep ? a.drop.scale : 0.f, ndelta);
+                            }
+                        }
 #pragma unroll
                         for (int i = 0; i < 4; ++i) ds[4 * hh + i] = s[kt][i] * (rs * dp[i]);
                     } else {
@@ -435,17 +451,27 @@ void attn_bwd_16bit(BwdArgs a) {
                     const f32x4 lse4 = as_f32x4(lds_ld16(slse + (qt * 16 + 4 * g) * 4));
                     const f32x4 ndelta4 = as_f32x4(lds_ld16(sdelta + (qt * 16 + 4 * g) * 4));
                     f32x4 sacc = M::mma(ld_op(sq + qt * 16 * RS, 0), kop[0], f32x4{0.f, 0.f, 0.f, 0.f});
-                    f32x4 dpacc = M::mma(ld_op(sdo + qt * 16 * RS, 0), vop[0], ndelta4);
+                    f32x4 dpacc = M::mma(ld_op(sdo + qt * 16 * RS, 0), vop[0], DROP ? f32x4{0.f, 0.f, 0.f, 0.f} : ndelta4);
 #pragma unroll
                     for (int i = 1; i < NI; ++i) {
                         sacc = M::mma(ld_op(sq + qt * 16 * RS, i), kop[i], sacc);
                         dpacc = M::mma(ld_op(sdo + qt * 16 * RS, i), vop[i], dpacc);
                     }
+                    f32x4 ms = f32x4{1.f, 1.f, 1.f, 1.f};  // dropout multiplier of each score
+                    if constexpr (DROP) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const uint64_t idx =
+                                (uint64_t)(((int64_t)b * a.H + h) * a.Sq + q0 + qt * 16 + 4 * g + i) * (uint64_t)a.Skv + key;
+                            ms[i] = drop_hash(idx, a.drop.k0, a.drop.k1) >= a.drop.thresh ? a.drop.scale : 0.f;
+                            dpacc[i] = __builtin_fmaf(dpacc[i], ms[i], ndelta4[i]);
+                        }
+                    }
                     if (full) {
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const float pv = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse4[i]));
-                            p[4 * hh + i] = pv;
+                            p[4 * hh + i] = DROP ? pv * ms[i] : pv;
                             ds[4 * hh + i] = pv * dpacc[i];
                         }
                     } else {
@@ -455,7 +481,7 @@ void attn_bwd_16bit(BwdArgs a) {
                             const bool ok = kok && q < Sqb && (!a.causal || key <= q0 + q);
                             const float pv = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse4[i]));
                             // 0 * lse: NaN only for a query that sees no key (lse = -inf)
-                            p[4 * hh + i] = ok ? pv : 0.f * lse4[i];
+                            p[4 * hh + i] = ok ? (DROP ? pv * ms[i] : pv) : 0.f * lse4[i];
                             ds[4 * hh + i] = ok ? pv * dpacc[i] : 0.f;
                         }
                     }
@@ -538,7 +564,7 @@ constexpr int bwd_occ_fp32() {
     return 2;
 }
 
-template <int D, int NKC, bool LOOP>
+template <int D, int NKC, bool LOOP, bool DROP = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(bwd_occ_fp32<D, NKC>(), 8)))
 void attn_bwd_fp32(BwdArgs a) {
     constexpr int CH4 = D / 4;    // 4-float chunks per row
@@ -738,16 +764,24 @@ void attn_bwd_fp32(BwdArgs a) {
                 lds_st4(sdelta + qrow * 4, __builtin_bit_cast(uint32_t, ndelta));
             }
             // scale * dS^T = P^T (dP^T - delta) * scale, dP^T = V dO^T
+            const uint64_t drow = DROP ? (uint64_t)(((int64_t)b * a.H + h) * a.Sq + qabs) * (uint64_t)a.Skv : 0;
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt) {
                 if (kt * 16 < kend) {
                     __builtin_amdgcn_sched_barrier(0);
-                    f32x4 dp = f32x4{ndelta, ndelta, ndelta, ndelta};
+                    f32x4 dp = DROP ? f32x4{0.f, 0.f, 0.f, 0.f} : f32x4{ndelta, ndelta, ndelta, ndelta};
 #pragma unroll
                     for (int i = 0; i < NI; ++i) {
                         const f32x4 vv = ld_chunk(lvq, kt * 16 + m, 4 * i + g);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) dp = mma_f32(vv[e], doop[i][e], dp);
+                    }
+                    if constexpr (DROP) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const bool keep = drop_hash(drow + (uint64_t)(kt * 16 + 4 * g + i), a.drop.k0, a.drop.k1) >= a.drop.thresh;
+                            dp[i] = __builtin_fmaf(dp[i], keep ? a.drop.scale : 0.f, ndelta);
+                        }
                     }
 #pragma unroll
                     for (int i = 0; i < 4; ++i) s[kt][i] = s[kt][i] * (rs * dp[i]);
@@ -793,7 +827,7 @@ void attn_bwd_fp32(BwdArgs a) {
                 const f32x4 lse4 = as_f32x4(lds_ld16(slse + (qt * 16 + 4 * g) * 4));
                 const f32x4 ndelta4 = as_f32x4(lds_ld16(sdelta + (qt * 16 + 4 * g) * 4));
                 f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
-                f32x4 dpacc = ndelta4;
+                f32x4 dpacc = DROP ? f32x4{0.f, 0.f, 0.f, 0.f} : ndelta4;
 #pragma unroll
                 for (int i = 0; i < NI; ++i) {
                     const f32x4 qa = ld_chunk(lq, qt * 16 + m, 4 * i + g);
@@ -804,13 +838,23 @@ void attn_bwd_fp32(BwdArgs a) {
                         dpacc = mma_f32(da[e], vop[i][e], dpacc);
                     }
                 }
+                f32x4 ms = f32x4{1.f, 1.f, 1.f, 1.f};  // dropout multiplier of each score
+                if constexpr (DROP) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint64_t idx =
+                            (uint64_t)(((int64_t)b * a.H + h) * a.Sq + q0 + qt * 16 + 4 * g + i) * (uint64_t)a.Skv + key;
+                        ms[i] = drop_hash(idx, a.drop.k0, a.drop.k1) >= a.drop.thresh ? a.drop.scale : 0.f;
+                        dpacc[i] = __builtin_fmaf(dpacc[i], ms[i], ndelta4[i]);
+                    }
+                }
                 float p[4], ds[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int q = qt * 16 + 4 * g + i;
                     const bool okq = kok && q < Sqb && (!a.causal || key <= q0 + q);
                     const float pv = fast_exp2(__builtin_fmaf(sacc[i], a.c2, -lse4[i]));
-                    p[i] = okq ? pv : 0.f * lse4[i];  // NaN only for a query that sees no key
+                    p[i] = okq ? (DROP ? pv * ms[i] : pv) : 0.f * lse4[i];  // NaN only for a query that sees no key
                     ds[i] = okq ? pv * dpacc[i] : 0.f;
                 }
                 // dV^T += dO^T P, dK^T += Q^T dS: k-step i covers queries 16qt + 4g' + i
@@ -880,5 +924,7 @@ inline int bwd_nkc_pow2(int nkc) { return nkc <= 1 ? 1 : nkc <= 2 ? 2 : nkc <= 4
 int dispatch_bwd16_loop(bool bf16, int D, int nkc, int grid, size_t lds, hipStream_t st, const BwdArgs& a);
 int dispatch_bwd_fp32(bool loop, int D, int nkc, int grid, size_t lds, hipStream_t st, const BwdArgs& a);
 int dispatch_bwd_fp32_loop(int D, int nkc, int grid, size_t lds, hipStream_t st, const BwdArgs& a);
+// atx_attn_bwd_drop.hip: the LOOP variants with dropout, head_dim 48 and 64.
+int dispatch_bwd_drop(int dtype, int D, int nkc, int grid, size_t lds, hipStream_t st, const BwdArgs& a);
 
 }  // namespace atx

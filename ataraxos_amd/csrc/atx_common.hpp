@@ -33,6 +33,52 @@ void clear_error();
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // ---------------------------------------------------------------------------
+// Attention dropout (host and device).
+// Element (b, h, i, j) of the [B, H, S_q, S_kv] attention weights is kept
+// when drop_hash(((b * H + h) * S_q + i) * S_kv + j) >= thresh, thresh =
+// floor(p * 2^32); kept weights are scaled by 1 / (1 - p).  The hash mixes
+// the index's two 32-bit halves with a 64-bit key derived from the caller's
+// (seed, offset) (splitmix64) and finishes with MurmurHash3's fmix32.  For a
+// fixed key and upper half the map from the lower 32 index bits to hashes is
+// a bijection.  The forward, the backward and atx_dropout_mask all call this
+// one function, so they agree on every element.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline uint32_t fmix32(uint32_t h) {
+    h ^= h >> 16;
+    h *= 0x85EBCA6Bu;
+    h ^= h >> 13;
+    h *= 0xC2B2AE35u;
+    h ^= h >> 16;
+    return h;
+}
+__host__ __device__ inline uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+struct DropKey {
+    uint32_t k0, k1;  // the 64-bit key's halves
+    uint32_t thresh;  // keep when hash >= thresh
+    float scale;      // 1 / (1 - p)
+};
+__host__ __device__ inline uint32_t drop_hash(uint64_t idx, uint32_t k0, uint32_t k1) {
+    uint32_t h = ((uint32_t)idx ^ k0) * 0x9E3779B1u;
+    h ^= ((uint32_t)(idx >> 32) ^ k1) * 0x85EBCA77u;
+    return fmix32(h);
+}
+inline DropKey make_drop_key(float p, uint64_t seed, uint64_t offset) {
+    const uint64_t key = splitmix64(seed ^ splitmix64(offset));
+    DropKey d;
+    d.k0 = (uint32_t)key;
+    d.k1 = (uint32_t)(key >> 32);
+    const double t = (double)p * 4294967296.0;
+    d.thresh = t >= 4294967295.0 ? 0xFFFFFFFFu : (uint32_t)t;
+    d.scale = p > 0.f ? 1.f / (1.f - p) : 1.f;
+    return d;
+}
+
+// ---------------------------------------------------------------------------
 // Device: vector types.
 // ---------------------------------------------------------------------------
 typedef float f32x4 __attribute__((ext_vector_type(4)));

@@ -18,6 +18,9 @@ outside the kernels' range raises.
 * :func:`mha_forward` — a whole self-attention layer (projections, attention,
   output projection) in one launch, ``stratego/networks/attention.py:152-204``.
 * :func:`attention_decode` — one query per (batch, head) against a KV cache.
+* :func:`dropout_mask` — the keep decisions of attention dropout (the
+  ``dropout_p`` / ``dropout_seed`` / ``dropout_offset`` arguments of the
+  attention functions) as a ``[B, H, S_q, S_kv]`` uint8 tensor.
 """
 
 from __future__ import annotations
@@ -37,6 +40,10 @@ _DTYPES = {
 
 MAX_SEQ_KV = 256
 HEAD_DIMS = (16, 32, 48, 64, 80, 96, 112, 128)
+# head_dims whose attention kernels are built with dropout (the reference
+# networks' 64 and 48)
+DROPOUT_HEAD_DIMS = (48, 64)
+_U64 = (1 << 64) - 1
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -94,9 +101,44 @@ def _padding_bytes(key_padding_mask: torch.Tensor | None, b: int, skv: int, ref:
             else (key_padding_mask != 0).view(torch.uint8)).contiguous()
 
 
-def attention_supported(head_dim: int, seq_kv: int, dtype: torch.dtype) -> bool:
-    """True when :func:`attention` covers this shape and dtype."""
+def attention_supported(head_dim: int, seq_kv: int, dtype: torch.dtype, dropout: bool = False) -> bool:
+    """True when :func:`attention` covers this shape and dtype (with
+    ``dropout``: with a nonzero ``dropout_p``)."""
+    if dropout and head_dim not in DROPOUT_HEAD_DIMS:
+        return False
     return dtype in _DTYPES and head_dim in HEAD_DIMS and 1 <= seq_kv <= MAX_SEQ_KV
+
+
+def _set_dropout(p, dropout_p: float, seed: int, offset: int) -> None:
+    if not 0.0 <= dropout_p < 1.0:
+        raise ValueError(f"dropout_p must be in [0, 1), got {dropout_p}")
+    p.dropout_p = float(dropout_p)
+    p.dropout_seed = int(seed) & _U64
+    p.dropout_offset = int(offset) & _U64
+
+
+def new_dropout_seed() -> int:
+    """A fresh 63-bit dropout seed from torch's default (CPU) generator, so
+    ``torch.manual_seed`` makes a dropout run repeatable."""
+    return int(torch.randint(0, 1 << 62, (1,), dtype=torch.int64).item())
+
+
+def dropout_mask(
+    batch: int, num_heads: int, seq_q: int, seq_kv: int, p: float, seed: int, offset: int = 0,
+    device: torch.device | str = "cuda",
+) -> torch.Tensor:
+    """``keep[b, h, i, j]`` (uint8, 1 = kept) of attention dropout with
+    ``(p, seed, offset)``: the decisions :func:`attention_forward` and
+    :func:`attention_backward` make for the same arguments.  One launch of
+    ``atx_dropout_mask``."""
+    if not 0.0 <= p < 1.0:
+        raise ValueError(f"dropout_mask: p must be in [0, 1), got {p}")
+    keep = torch.empty((batch, num_heads, seq_q, seq_kv), dtype=torch.uint8, device=device)
+    _require_device("dropout_mask", keep)
+    rc = _lib.load().atx_dropout_mask(batch, num_heads, seq_q, seq_kv, float(p), int(seed) & _U64,
+                                      int(offset) & _U64, keep.data_ptr(), _stream(keep))
+    _lib.check(rc, "atx_dropout_mask")
+    return keep
 
 
 def attention_forward(
@@ -107,11 +149,19 @@ def attention_forward(
     scale: float | None = None,
     key_padding_mask: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
+    dropout_p: float = 0.0,
+    dropout_seed: int = 0,
+    dropout_offset: int = 0,
 ) -> torch.Tensor:
     """Forward only (no autograd).  q ``[B, S_q, H, D]``, k/v ``[B, S_kv, H_kv, D]``.
 
     ``key_padding_mask`` is ``[B, S_kv]`` bool, True = ignore the key (the
     ``key_padding_mask`` convention of ``torch.nn.MultiheadAttention``).
+    ``dropout_p > 0`` (head_dim 48 or 64) drops each softmax weight with
+    that probability and scales the rest by ``1 / (1 - dropout_p)``, as
+    ``nn.Dropout`` on the weights does (attention.py:312-313); the decisions
+    are a function of ``(dropout_seed, dropout_offset)`` and the weight's
+    index (:func:`dropout_mask`).
     Returns ``[B, S_q, H, D]`` contiguous in q's dtype.
     """
     _require_device("attention", q, k, v)
@@ -146,6 +196,7 @@ def attention_forward(
     p.causal = 1 if causal else 0
     p.key_pad = pad.data_ptr() if pad is not None else None
     p.key_pad_stride_b = pad.stride(0) if pad is not None else 0
+    _set_dropout(p, dropout_p, dropout_seed, dropout_offset)
     _lib.check(_lib.call("atx_attn_fwd", p, _stream(q)), "atx_attn_fwd")
     return out
 
@@ -191,24 +242,27 @@ def _pow2_chunks(nkc: int) -> int:
 
 
 def attention_backward_plan(
-    head_dim: int, seq_q: int, seq_kv: int, num_heads: int, num_kv_heads: int, dtype: torch.dtype
+    head_dim: int, seq_q: int, seq_kv: int, num_heads: int, num_kv_heads: int, dtype: torch.dtype,
+    dropout: bool = False,
 ) -> dict | None:
     """How ``atx_attn_bwd`` runs this shape (the library's own rule, restated):
     ``{"loop": bool, "key_chunks": int, "query_block": int, "lds": int}``, or
     None when the kernels do not cover it.  ``loop`` is the variant that runs
     the query heads of a KV group and blocks of ``query_block`` query rows one
-    after another (grouped-query attention, more than 256 queries, or more
-    query rows than LDS holds at once)."""
+    after another (grouped-query attention, more than 256 queries, more query
+    rows than LDS holds at once, or ``dropout``: a nonzero ``dropout_p``,
+    head_dim 48 or 64 only)."""
     if (dtype not in _ATTN_BWD_DTYPES or num_kv_heads < 1 or num_heads % num_kv_heads
             or head_dim % 16 or not 16 <= head_dim <= 128 or not 1 <= seq_kv <= MAX_SEQ_KV
-            or not 1 <= seq_q <= (1 << 20)):
+            or not 1 <= seq_q <= (1 << 20) or (dropout and head_dim not in DROPOUT_HEAD_DIMS)):
         return None
     fp32 = dtype == torch.float32
     qalign = 16 if fp32 else 32
     rq_all = -(-seq_q // qalign) * qalign
     exact = -(-seq_kv // 32)
     nkc = _pow2_chunks(exact) if fp32 else exact
-    loop = num_heads != num_kv_heads or seq_q > 256 or _bwd_lds_bytes(head_dim, rq_all, seq_kv, fp32, nkc) > _LDS_BYTES
+    loop = (dropout or num_heads != num_kv_heads or seq_q > 256
+            or _bwd_lds_bytes(head_dim, rq_all, seq_kv, fp32, nkc) > _LDS_BYTES)
     qb = 0
     if loop:
         nkc = _pow2_chunks(exact)
@@ -222,13 +276,15 @@ def attention_backward_plan(
 
 
 def attention_backward_supported(
-    head_dim: int, seq_q: int, seq_kv: int, num_heads: int, num_kv_heads: int, dtype: torch.dtype
+    head_dim: int, seq_q: int, seq_kv: int, num_heads: int, num_kv_heads: int, dtype: torch.dtype,
+    dropout: bool = False,
 ) -> bool:
     """True when :func:`attention_backward` covers this shape and dtype:
     bf16 / fp16 / fp32, GQA included, head_dim a multiple of 16 up to 128, up
     to 256 keys and any number of queries; fp32 with head_dim >= 80 only up
-    to 128 keys (its K and V rows must fit in LDS)."""
-    return attention_backward_plan(head_dim, seq_q, seq_kv, num_heads, num_kv_heads, dtype) is not None
+    to 128 keys (its K and V rows must fit in LDS); with dropout head_dim 48
+    or 64."""
+    return attention_backward_plan(head_dim, seq_q, seq_kv, num_heads, num_kv_heads, dtype, dropout) is not None
 
 
 def attention_backward(
@@ -240,6 +296,9 @@ def attention_backward(
     causal: bool = False,
     scale: float | None = None,
     key_padding_mask: torch.Tensor | None = None,
+    dropout_p: float = 0.0,
+    dropout_seed: int = 0,
+    dropout_offset: int = 0,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Gradients ``(dq, dk, dv)`` of :func:`attention_forward` for the
     upstream gradient ``grad_out``, given its inputs and its output ``out``
@@ -247,8 +306,11 @@ def attention_backward(
     fp16 or fp32).  One kernel launch; the softmax is recomputed from Q and K,
     so nothing but the output is kept from the forward.  With grouped-query
     attention, dk and dv sum the gradients of the query heads that share a KV
-    head (``repeat_interleave``, attention.py:210-220).  Returns contiguous
-    tensors in the inputs' dtype, dk / dv with H_kv heads."""
+    head (``repeat_interleave``, attention.py:210-220).  A forward run with
+    dropout passes the same ``dropout_p``, ``dropout_seed`` and
+    ``dropout_offset``: the kernel recomputes the same keep decisions.
+    Returns contiguous tensors in the inputs' dtype, dk / dv with H_kv
+    heads."""
     _require_device("attention_backward", q, k, v, out, grad_out)
     if not (q.dtype == k.dtype == v.dtype == out.dtype == grad_out.dtype):
         raise ValueError("attention_backward: mixed dtypes")
@@ -257,9 +319,10 @@ def attention_backward(
     if (tuple(k.shape) != (b, skv, hkv, d) or tuple(v.shape) != (b, skv, hkv, d)
             or tuple(out.shape) != (b, sq, h, d) or tuple(grad_out.shape) != (b, sq, h, d)):
         raise ValueError("attention_backward: shape mismatch")
-    if not attention_backward_supported(d, sq, skv, h, hkv, q.dtype):
+    if not attention_backward_supported(d, sq, skv, h, hkv, q.dtype, dropout_p > 0.0):
         raise NotImplementedError(
-            f"attention_backward: {q.dtype}, heads {h}/{hkv}, head_dim {d}, seq {sq}x{skv} not covered by the kernel"
+            f"attention_backward: {q.dtype}, heads {h}/{hkv}, head_dim {d}, seq {sq}x{skv}"
+            f"{', dropout' if dropout_p > 0.0 else ''} not covered by the kernel"
         )
     q, k, v, out, grad_out = (_aligned_rows(t) for t in (q, k, v, out, grad_out))
     pad = _padding_bytes(key_padding_mask, b, skv, q)
@@ -281,6 +344,7 @@ def attention_backward(
     p.causal = 1 if causal else 0
     p.key_pad = pad.data_ptr() if pad is not None else None
     p.key_pad_stride_b = pad.stride(0) if pad is not None else 0
+    _set_dropout(p, dropout_p, dropout_seed, dropout_offset)
     _lib.check(_lib.call("atx_attn_bwd", p, _stream(q)), "atx_attn_bwd")
     return dq, dk, dv
 
@@ -290,29 +354,37 @@ class _HipAttention(torch.autograd.Function):
     and fp32, GQA included).  The one shape family the backward kernels do
     not hold in LDS -- fp32 with head_dim >= 80 and more than 128 keys, which
     no network of the reference uses -- takes its gradients from an fp32
-    recomputation with torch ops on the same device."""
+    recomputation with torch ops on the same device.  With dropout only the
+    seed and offset are kept: the backward recomputes the keep decisions."""
 
     @staticmethod
-    def forward(ctx, q, k, v, causal, scale, key_padding_mask):  # type: ignore[override]
-        out = attention_forward(q, k, v, causal=causal, scale=scale, key_padding_mask=key_padding_mask)
+    def forward(ctx, q, k, v, causal, scale, key_padding_mask, dropout_p, seed, offset):  # type: ignore[override]
+        out = attention_forward(q, k, v, causal=causal, scale=scale, key_padding_mask=key_padding_mask,
+                                dropout_p=dropout_p, dropout_seed=seed, dropout_offset=offset)
         ctx.save_for_backward(q, k, v, out)
         ctx.causal, ctx.scale, ctx.kpm = causal, scale, key_padding_mask
+        ctx.drop = (dropout_p, seed, offset)
         return out
 
     @staticmethod
     def backward(ctx, grad_out):  # type: ignore[override]
         q, k, v, out = ctx.saved_tensors
         b, sq, h, d = q.shape
-        if attention_backward_supported(d, sq, k.shape[1], h, k.shape[2], q.dtype):
-            dq, dk, dv = attention_backward(q, k, v, out, grad_out.to(q.dtype), ctx.causal, ctx.scale, ctx.kpm)
-            return dq, dk, dv, None, None, None
+        dropout_p, seed, offset = ctx.drop
+        none = (None,) * 6
+        if attention_backward_supported(d, sq, k.shape[1], h, k.shape[2], q.dtype, dropout_p > 0.0):
+            dq, dk, dv = attention_backward(q, k, v, out, grad_out.to(q.dtype), ctx.causal, ctx.scale, ctx.kpm,
+                                            dropout_p, seed, offset)
+            return (dq, dk, dv, *none)
+        if dropout_p > 0.0:  # the forward accepted it, so the backward covers it: not reached
+            raise NotImplementedError("attention backward with dropout: shape not covered by the kernel")
         with torch.enable_grad():
             qf = q.detach().float().requires_grad_(True)
             kf = k.detach().float().requires_grad_(True)
             vf = v.detach().float().requires_grad_(True)
             o = _attention_reference_fp32(qf, kf, vf, ctx.causal, ctx.scale, ctx.kpm)
             gq, gk, gv = torch.autograd.grad(o, (qf, kf, vf), grad_out.float())
-        return gq.to(q.dtype), gk.to(k.dtype), gv.to(v.dtype), None, None, None
+        return (gq.to(q.dtype), gk.to(k.dtype), gv.to(v.dtype), *none)
 
 
 def attention(
@@ -322,13 +394,23 @@ def attention(
     causal: bool = False,
     scale: float | None = None,
     key_padding_mask: torch.Tensor | None = None,
+    dropout_p: float = 0.0,
+    dropout_seed: int | None = None,
+    dropout_offset: int = 0,
 ) -> torch.Tensor:
-    """Fused attention on BSHD tensors, with autograd (see :func:`attention_forward`)."""
+    """Fused attention on BSHD tensors, with autograd (see :func:`attention_forward`).
+
+    With ``dropout_p > 0`` and no ``dropout_seed`` a seed is drawn from
+    torch's default generator (:func:`new_dropout_seed`)."""
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
+    if dropout_p > 0.0 and dropout_seed is None:
+        dropout_seed = new_dropout_seed()
+    seed = 0 if dropout_seed is None else dropout_seed
     if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
-        return _HipAttention.apply(q, k, v, causal, scale, key_padding_mask)
-    return attention_forward(q, k, v, causal=causal, scale=scale, key_padding_mask=key_padding_mask)
+        return _HipAttention.apply(q, k, v, causal, scale, key_padding_mask, dropout_p, seed, dropout_offset)
+    return attention_forward(q, k, v, causal=causal, scale=scale, key_padding_mask=key_padding_mask,
+                             dropout_p=dropout_p, dropout_seed=seed, dropout_offset=dropout_offset)
 
 
 def kq_policy(

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ATX_ABI_VERSION 2
+#define ATX_ABI_VERSION 3
 
 /* Return codes. */
 #define ATX_OK 0
@@ -85,6 +85,18 @@ typedef struct AtxAttnParams {
     int32_t causal;          /* nonzero: mask j > s */
     const uint8_t* key_pad;  /* optional [batch, seq_kv]; nonzero = ignore key */
     int64_t key_pad_stride_b;
+    /* Attention dropout (training; attention.py:312-313 and FA2's
+     * dropout_p, :236-253): each softmax weight (b, h, i, j) is zeroed with
+     * probability dropout_p and the survivors scaled by 1 / (1 - dropout_p).
+     * The keep decision is a hash of the element's flat index
+     * ((b * H + h) * seq_q + i) * seq_kv + j and (dropout_seed,
+     * dropout_offset); atx_dropout_mask writes the same decisions, and
+     * atx_attn_bwd given the same three values differentiates through them.
+     * 0 <= dropout_p < 1; dropout_p > 0 needs head_dim 48 or 64. */
+    float dropout_p;
+    int32_t reserved_dropout; /* 0 */
+    uint64_t dropout_seed;
+    uint64_t dropout_offset;
 } AtxAttnParams;
 
 /*
@@ -135,6 +147,12 @@ typedef struct AtxAttnBwdParams {
     int32_t causal;
     const uint8_t* key_pad; /* optional [batch, seq_kv]; nonzero = ignore key */
     int64_t key_pad_stride_b;
+    /* The forward's dropout (see AtxAttnParams): the same dropout_p,
+     * dropout_seed and dropout_offset, and o the forward's output with it. */
+    float dropout_p;
+    int32_t reserved_dropout; /* 0 */
+    uint64_t dropout_seed;
+    uint64_t dropout_offset;
 } AtxAttnBwdParams;
 
 /*
@@ -156,6 +174,18 @@ typedef struct AtxAttnBwdParams {
  * all -inf row does.
  */
 int atx_attn_bwd(const AtxAttnBwdParams* params, void* stream);
+
+/*
+ * keep[b, h, i, j] = 1 where attention dropout with (p, seed, offset) keeps
+ * weight (b, h, i, j) of a [batch, num_heads, seq_q, seq_kv] attention, else
+ * 0: the decisions atx_attn_fwd / atx_attn_bwd make.  `keep` is a contiguous
+ * uint8 device buffer of batch * num_heads * seq_q * seq_kv bytes.
+ * Asynchronous on `stream`.  No counterpart in the reference (its math path
+ * returns no mask; FA2 returns one only in debug mode): for checking a
+ * dropout run against an explicit mask.
+ */
+int atx_dropout_mask(int32_t batch, int32_t num_heads, int32_t seq_q, int32_t seq_kv, float p, uint64_t seed,
+                     uint64_t offset, uint8_t* keep, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Key-query policy head: logits + legal-move mask (+ softmax)              */

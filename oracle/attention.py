@@ -37,6 +37,7 @@ def attention(
     causal: bool = False,
     scale: float | None = None,
     key_pad: np.ndarray | None = None,
+    drop: np.ndarray | None = None,
 ) -> np.ndarray:
     """BSHD attention in float64.
 
@@ -47,9 +48,12 @@ def attention(
     ``(Q K^T) * (1/sqrt(D))`` with the scale applied after the product
     (:300-301), top-left causal mask ``triu(ones(S_q, S_kv), 1) -> -inf``
     (:303-308), softmax over keys (:310), ``P V`` and back to BSHD (:315-316).
-    Dropout (:312-313) is inference-off and not restated.  ``key_pad``
-    (``[B, S_kv]``, True = ignore) adds the key-padding mask the Belief
-    decoder passes as ``memory_key_padding_mask`` (belief_net.py:159,172-177).
+    ``drop`` (``[B, H, S_q, S_kv]``: ``keep / (1 - p)``, e.g. from
+    :func:`oracle.dropout.keep_mask`) multiplies the softmax weights before
+    ``P V``, as ``F.dropout`` on them does in training (:312-313); None is
+    inference.  ``key_pad`` (``[B, S_kv]``, True = ignore) adds the
+    key-padding mask the Belief decoder passes as ``memory_key_padding_mask``
+    (belief_net.py:159,172-177).
     """
     q64 = np.asarray(q, dtype=np.float64).transpose(0, 2, 1, 3)
     k64 = np.asarray(k, dtype=np.float64).transpose(0, 2, 1, 3)
@@ -66,7 +70,10 @@ def attention(
         scores = np.where(above, NEG_INF, scores)
     if key_pad is not None:
         scores = np.where(np.asarray(key_pad, dtype=bool)[:, None, None, :], NEG_INF, scores)
-    return np.matmul(softmax_lastdim(scores), v64).transpose(0, 2, 1, 3)
+    probs = softmax_lastdim(scores)
+    if drop is not None:
+        probs = probs * np.asarray(drop, dtype=np.float64)
+    return np.matmul(probs, v64).transpose(0, 2, 1, 3)
 
 
 def attention_backward(
@@ -77,6 +84,7 @@ def attention_backward(
     causal: bool = False,
     scale: float | None = None,
     key_pad: np.ndarray | None = None,
+    drop: np.ndarray | None = None,
 ) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     """Gradients ``(dq, dk, dv)`` of :func:`attention` for the upstream
     gradient ``d_o`` (``[B, S_q, H, D]``), in float64.
@@ -93,7 +101,9 @@ def attention_backward(
     heads that share a KV head.  An all-masked row has ``P = NaN`` (as in the
     forward): its ``dS`` is still 0 (every entry is masked), so it adds 0 to
     ``dq`` and ``dk``, but ``dV = P^T dO`` makes the whole ``(batch, head)``
-    slice of ``dv`` NaN -- what autograd through that math gives.
+    slice of ``dv`` NaN -- what autograd through that math gives.  With
+    ``drop`` (the forward's dropout multipliers M) the weights that reach V
+    are ``P o M``: ``dV = (P o M)^T dO`` and the softmax sees ``dP o M``.
     """
     q64 = np.asarray(q, dtype=np.float64).transpose(0, 2, 1, 3)
     k64 = np.asarray(k, dtype=np.float64).transpose(0, 2, 1, 3)
@@ -112,9 +122,12 @@ def attention_backward(
     if key_pad is not None:
         masked = masked | np.asarray(key_pad, dtype=bool)[:, None, None, :]
     p = softmax_lastdim(np.where(masked, NEG_INF, scores))
+    mult = None if drop is None else np.asarray(drop, dtype=np.float64)
     with np.errstate(invalid="ignore"):
-        dv = np.matmul(p.swapaxes(-1, -2), g64)
+        dv = np.matmul(p.swapaxes(-1, -2) if mult is None else (p * mult).swapaxes(-1, -2), g64)
         dp = np.matmul(g64, ve.swapaxes(-1, -2))
+        if mult is not None:
+            dp = dp * mult
         ds = np.where(masked, 0.0, p * (dp - np.sum(dp * p, axis=-1, keepdims=True)))
         dq = np.matmul(ds, ke) * scale
         dk = np.matmul(ds.swapaxes(-1, -2), q64) * scale

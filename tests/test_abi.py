@@ -130,6 +130,11 @@ def test_attention_validation_codes():
     _expect("atx_attn_fwd", _attn_params(o_stride_s=32), _lib.ERR_INVALID_ARGUMENT, "overlap")
     _expect("atx_attn_fwd", _attn_params(k_stride_s=-384), _lib.ERR_UNSUPPORTED, ">= 0")
     _expect("atx_attn_fwd", _attn_params(v_stride_s=1 << 26), _lib.ERR_UNSUPPORTED, "2 GiB")
+    _expect("atx_attn_fwd", _attn_params(dropout_p=1.0), _lib.ERR_INVALID_ARGUMENT, "dropout_p")
+    _expect("atx_attn_fwd", _attn_params(dropout_p=-0.1), _lib.ERR_INVALID_ARGUMENT, "dropout_p")
+    _expect("atx_attn_fwd", _attn_params(dropout_p=float("nan")), _lib.ERR_INVALID_ARGUMENT, "dropout_p")
+    _expect("atx_attn_fwd", _attn_params(dropout_p=0.1, head_dim=32, q_stride_h=32, k_stride_h=32, v_stride_h=32,
+                                         o_stride_h=32), _lib.ERR_UNSUPPORTED, "dropout needs head_dim")
 
 
 def _bwd_params(**kw) -> _lib.AttnBwdParams:
@@ -168,6 +173,30 @@ def test_attention_backward_validation_codes():
     _expect("atx_attn_bwd", _bwd_params(dv_stride_s=32), _lib.ERR_INVALID_ARGUMENT, "overlap")
     _expect("atx_attn_bwd", _bwd_params(dtype=_lib.DTYPE_FP32, head_dim=128, seq_q=256, seq_kv=256, **{
         f"{n}_stride_s": 768 for n in ("q", "k", "v", "o", "do", "dq", "dk", "dv")}), _lib.ERR_UNSUPPORTED, "LDS")
+    _expect("atx_attn_bwd", _bwd_params(dropout_p=1.0), _lib.ERR_INVALID_ARGUMENT, "dropout_p")
+    _expect("atx_attn_bwd", _bwd_params(dropout_p=0.2, head_dim=96, **{
+        f"{n}_stride_h": 96 for n in ("q", "k", "v", "o", "do", "dq", "dk", "dv")}), _lib.ERR_UNSUPPORTED,
+        "dropout needs head_dim")
+
+
+def test_dropout_mask_validation_codes():
+    lib = _lib.load()
+    fake = 1 << 20  # never dereferenced: every case below fails validation first
+    for args, text in [((0, 1, 4, 4, 0.1, 1, 0, fake), "sizes"), ((1, 1, 4, 4, 1.0, 1, 0, fake), "[0, 1)"),
+                       ((1, 1, 4, 4, float("nan"), 1, 0, fake), "[0, 1)"), ((1, 1, 4, 4, 0.1, 1, 0, None), "NULL")]:
+        assert lib.atx_dropout_mask(*args, None) == _lib.ERR_INVALID_ARGUMENT
+        assert text in _lib.last_error()
+
+
+def test_dropout_forces_the_loop_backward():
+    from ataraxos_amd import ops
+
+    plan = ops.attention_backward_plan(64, 101, 101, 6, 6, torch.bfloat16, dropout=True)
+    assert plan is not None and plan["loop"] and plan["key_chunks"] == 4
+    assert not ops.attention_backward_plan(64, 101, 101, 6, 6, torch.bfloat16)["loop"]
+    assert ops.attention_backward_plan(32, 101, 101, 6, 6, torch.bfloat16, dropout=True) is None
+    assert ops.attention_supported(48, 101, torch.float32, dropout=True)
+    assert not ops.attention_supported(128, 101, torch.float32, dropout=True)
 
 
 def test_backward_lds_rule_matches_python_predicate():
@@ -232,7 +261,7 @@ def test_policy_backward_validation_codes():
     p.scale = 0.125
     assert _lib.load().atx_kq_bwd(None, None) == _lib.ERR_INVALID_ARGUMENT
     for field, value, code, text in [
-        ("abi_version", 3, _lib.ERR_ABI, "abi_version"),
+        ("abi_version", 99, _lib.ERR_ABI, "abi_version"),
         ("dtype", 9, _lib.ERR_INVALID_ARGUMENT, "dtype"),
         ("out_mode", 5, _lib.ERR_INVALID_ARGUMENT, "out_mode"),
         ("out_mode", _lib.KQ_OUT_PROBS, _lib.ERR_INVALID_ARGUMENT, "null"),  # probs mode needs probs
@@ -262,7 +291,7 @@ def test_fused_layer_validation_codes():
     assert _lib.load().atx_mha_fwd(None, None) == _lib.ERR_INVALID_ARGUMENT
     assert _lib.load().atx_mha_fwd_packed(None, None) == _lib.ERR_INVALID_ARGUMENT
     for (field, value, code, text), name in itertools.product([
-        ("abi_version", 3, _lib.ERR_ABI, "abi_version"),
+        ("abi_version", 99, _lib.ERR_ABI, "abi_version"),
         ("dtype", _lib.DTYPE_FP32, _lib.ERR_UNSUPPORTED, "fp32"),
         ("embed_dim", 400, _lib.ERR_UNSUPPORTED, "head_dim"),
         ("num_heads", 3, _lib.ERR_UNSUPPORTED, "head_dim"),

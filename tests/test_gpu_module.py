@@ -19,8 +19,10 @@ def test_backend_is_hip_on_gpu(cuda):
     assert m.backend == "hip"
     m.train()
     assert m.backend == "hip"  # dropout 0: the kernel still runs in training
-    md = MultiHeadAttention(512, 8, dropout=0.2).to(cuda)
-    assert md.eval().backend == "hip" and md.train().backend == "math"
+    md = MultiHeadAttention(512, 8, dropout=0.2).to(cuda)  # head_dim 64: the kernels' own dropout
+    assert md.eval().backend == "hip" and md.train().backend == "hip"
+    m32 = MultiHeadAttention(256, 8, dropout=0.2).to(cuda)  # head_dim 32: no dropout kernels
+    assert m32.eval().backend == "hip" and m32.train().backend == "math"
 
 
 def test_fp32_module_matches_oracle(cuda):
