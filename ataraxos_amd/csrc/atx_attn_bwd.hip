@@ -125,8 +125,8 @@ extern "C" int atx_attn_bwd(const AtxAttnBwdParams* p, void* stream) {
 
     // Variant: every query staged at once (one pass), or LOOP -- query heads
     // of a group and blocks of QB query rows one after another (GQA, or too
-    // many query rows for LDS; dropout, whose kernels are built as LOOP
-    // only).  The LOOP and fp32 variants exist for 1, 2, 4 and 8 key chunks.
+    // many query rows for LDS).  The LOOP and fp32 variants exist for 1, 2, 4
+    // and 8 key chunks.
     const bool gqa = p->num_heads != p->num_kv_heads;
     const size_t kLds = 160 * 1024;
     const int nkc_exact = (p->seq_kv + 31) / 32;
@@ -136,7 +136,7 @@ extern "C" int atx_attn_bwd(const AtxAttnBwdParams* p, void* stream) {
         return f32 ? bwd_lds_bytes_fp32(D, nkc_ * 32, rq_) : bwd_lds_bytes(D, nkc_ * 32, rq_);
     };
     int nkc = f32 ? bwd_nkc_pow2(nkc_exact) : nkc_exact;
-    const bool loop = drop || gqa || p->seq_q > 256 || lds_of(nkc, rq_all) > kLds;
+    const bool loop = gqa || p->seq_q > 256 || lds_of(nkc, rq_all) > kLds;
     int qb = 0;
     if (loop) {
         nkc = bwd_nkc_pow2(nkc_exact);
@@ -169,7 +169,7 @@ extern "C" int atx_attn_bwd(const AtxAttnBwdParams* p, void* stream) {
     a.causal = p->causal != 0;
     a.drop = make_drop_key(drop ? p->dropout_p : 0.f, p->dropout_seed, p->dropout_offset);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (drop) return dispatch_bwd_drop(p->dtype, D, nkc, (int)grid, lds, st, a);
+    if (drop) return dispatch_bwd_drop(p->dtype, loop, D, nkc, (int)grid, lds, st, a);
     if (f32) return dispatch_bwd_fp32(loop, D, nkc, (int)grid, lds, st, a);
     if (loop) return dispatch_bwd16_loop(p->dtype == ATX_DTYPE_BF16, D, nkc, (int)grid, lds, st, a);
     if (p->dtype == ATX_DTYPE_BF16) return dispatch_bwd16<__bf16>(D, nkc, (int)grid, lds, st, a);

@@ -85,7 +85,7 @@ constexpr int bwd_occ() {
 // and over all queries, without atomics.  dQ rows are complete per block
 // (every key is resident).
 //
-// DROP (attention dropout, LOOP variants only): the forward used P' = P o M,
+// DROP (attention dropout): the forward used P' = P o M,
 // M = keep / (1 - p) from drop_hash.  dV = P'^T dO, and with dP' = dO V^T,
 // dS = P o (M o dP' - delta); delta = rowsum(P o M o dP') = rowsum(O o dO)
 // with O the forward's dropout output, so delta is unchanged.  The dP'
@@ -924,7 +924,9 @@ inline int bwd_nkc_pow2(int nkc) { return nkc <= 1 ? 1 : nkc <= 2 ? 2 : nkc <= 4
 int dispatch_bwd16_loop(bool bf16, int D, int nkc, int grid, size_t lds, hipStream_t st, const BwdArgs& a);
 int dispatch_bwd_fp32(bool loop, int D, int nkc, int grid, size_t lds, hipStream_t st, const BwdArgs& a);
 int dispatch_bwd_fp32_loop(int D, int nkc, int grid, size_t lds, hipStream_t st, const BwdArgs& a);
-// atx_attn_bwd_drop.hip: the LOOP variants with dropout, head_dim 48 and 64.
-int dispatch_bwd_drop(int dtype, int D, int nkc, int grid, size_t lds, hipStream_t st, const BwdArgs& a);
+// atx_attn_bwd_drop.hip / atx_attn_bwd_drop_fp32.hip: both variants with
+// dropout, head_dim 48 and 64.
+int dispatch_bwd_drop(int dtype, bool loop, int D, int nkc, int grid, size_t lds, hipStream_t st, const BwdArgs& a);
+int dispatch_bwd_drop_fp32(bool loop, int D, int nkc, int grid, size_t lds, hipStream_t st, const BwdArgs& a);
 
 }  // namespace atx

@@ -249,9 +249,9 @@ def attention_backward_plan(
     ``{"loop": bool, "key_chunks": int, "query_block": int, "lds": int}``, or
     None when the kernels do not cover it.  ``loop`` is the variant that runs
     the query heads of a KV group and blocks of ``query_block`` query rows one
-    after another (grouped-query attention, more than 256 queries, more query
-    rows than LDS holds at once, or ``dropout``: a nonzero ``dropout_p``,
-    head_dim 48 or 64 only)."""
+    after another (grouped-query attention, more than 256 queries, or more
+    query rows than LDS holds at once).  ``dropout`` (a nonzero
+    ``dropout_p``) runs the same plan, at head_dim 48 or 64 only."""
     if (dtype not in _ATTN_BWD_DTYPES or num_kv_heads < 1 or num_heads % num_kv_heads
             or head_dim % 16 or not 16 <= head_dim <= 128 or not 1 <= seq_kv <= MAX_SEQ_KV
             or not 1 <= seq_q <= (1 << 20) or (dropout and head_dim not in DROPOUT_HEAD_DIMS)):
@@ -261,8 +261,7 @@ def attention_backward_plan(
     rq_all = -(-seq_q // qalign) * qalign
     exact = -(-seq_kv // 32)
     nkc = _pow2_chunks(exact) if fp32 else exact
-    loop = (dropout or num_heads != num_kv_heads or seq_q > 256
-            or _bwd_lds_bytes(head_dim, rq_all, seq_kv, fp32, nkc) > _LDS_BYTES)
+    loop = num_heads != num_kv_heads or seq_q > 256 or _bwd_lds_bytes(head_dim, rq_all, seq_kv, fp32, nkc) > _LDS_BYTES
     qb = 0
     if loop:
         nkc = _pow2_chunks(exact)

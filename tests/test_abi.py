@@ -188,12 +188,14 @@ def test_dropout_mask_validation_codes():
         assert text in _lib.last_error()
 
 
-def test_dropout_forces_the_loop_backward():
+def test_dropout_backward_plan():
     from ataraxos_amd import ops
 
-    plan = ops.attention_backward_plan(64, 101, 101, 6, 6, torch.bfloat16, dropout=True)
-    assert plan is not None and plan["loop"] and plan["key_chunks"] == 4
-    assert not ops.attention_backward_plan(64, 101, 101, 6, 6, torch.bfloat16)["loop"]
+    for d in ops.DROPOUT_HEAD_DIMS:
+        for dt in (torch.bfloat16, torch.float32):
+            for sq, h, hkv in ((101, 6, 6), (300, 8, 8), (64, 8, 2)):
+                assert (ops.attention_backward_plan(d, sq, 101, h, hkv, dt, dropout=True)
+                        == ops.attention_backward_plan(d, sq, 101, h, hkv, dt))
     assert ops.attention_backward_plan(32, 101, 101, 6, 6, torch.bfloat16, dropout=True) is None
     assert ops.attention_supported(48, 101, torch.float32, dropout=True)
     assert not ops.attention_supported(128, 101, torch.float32, dropout=True)
