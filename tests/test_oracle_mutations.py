@@ -200,3 +200,36 @@ def test_policy_backward_mistakes_are_caught_by_torch_autograd():
     unmasked = g.reshape(b, s, s) @ k * scale  # mutant: gradient reaches illegal entries
     np.testing.assert_allclose(kq_backward(q, k, mask, scale, g)[0], tq2.grad.numpy(), rtol=1e-10, atol=1e-12)
     assert not np.allclose(unmasked, tq2.grad.numpy(), atol=1e-6)
+
+
+def test_dropout_mistakes_are_caught():
+    """Dropout: renormalising over the kept weights (a softmax of the dropped
+    scores), or a backward that leaves the mask out of dP, disagree with
+    torch float64 autograd on the same explicit mask; a hash whose upper
+    index word is ignored repeats the mask every 2^32 weights."""
+    from oracle.dropout import drop_hash, drop_key, keep_mask
+
+    b, s, h, d, p = 1, 12, 2, 8, 0.3
+    q, k, v, g = (rnd(b, s, h, d, seed=i) for i in range(4))
+    keep = keep_mask(b, h, s, s, p, seed=3, offset=0)
+    mult = keep / (1 - p)
+    tq, tk, tv = (torch.from_numpy(x).transpose(1, 2).requires_grad_(True) for x in (q, k, v))
+    probs = torch.softmax(tq @ tk.transpose(-1, -2) / np.sqrt(d), dim=-1) * torch.from_numpy(mult)
+    o = (probs @ tv).transpose(1, 2)
+    o.backward(torch.from_numpy(g))
+    want_o = o.detach().numpy()
+    # renormalised over kept weights
+    sc = _bhsd(q) @ _bhsd(k).swapaxes(-1, -2) / np.sqrt(d)
+    renorm = (softmax_lastdim(np.where(keep, sc, -np.inf)) @ _bhsd(v)).transpose(0, 2, 1, 3)
+    assert np.abs(renorm - want_o).max() > 1e-3
+    np.testing.assert_allclose(attention(q, k, v, drop=mult), want_o, rtol=1e-12, atol=1e-12)
+    # backward without the mask on dP: what attention_backward would give if
+    # dropout only touched dV
+    dq_mut = attention_backward(q, k, v, g)[0]
+    assert np.abs(dq_mut - tq.grad.transpose(1, 2).numpy()).max() > 1e-3
+    np.testing.assert_allclose(attention_backward(q, k, v, g, drop=mult)[0], tq.grad.transpose(1, 2).numpy(),
+                               rtol=1e-10, atol=1e-12)
+    # the upper index word matters
+    k0, k1, _, _ = drop_key(p, 3, 0)
+    lo = np.arange(4096, dtype=np.uint64)
+    assert (drop_hash(lo, k0, k1) != drop_hash(lo + np.uint64(1 << 32), k0, k1)).mean() > 0.99
