@@ -19,16 +19,14 @@
 // SIMDs.  Every wave also owns 3 of the 24 feature tiles of Y in registers
 // and adds Wo[:, 64h ..] O_h^T into them one step after head h's attention.
 //
-// A sample takes 7 steps s = 0..6:
-//   1. all waves: out-projection of head s - 2 (slot s & 1); at step 0 of any
-//      sample but the workgroup's first, the previous sample's head 5, then
-//      that sample's Y store;
-//   2. producers, s < 6: the MFMAs of head s (registers only); s = 6: the next
-//      sample's X rows into LDS.  Consumers, s >= 1: attention of head s - 1;
-//   3. barrier; then, s < 6, producers store head s into slot s & 1, barrier.
-// Slot s & 1 was last read in step s's part 1 (the out-projection of head
-// s - 2) and before that by the attention of head s - 2 in step s - 1, both
-// before step s's first barrier; X was last read by the producers in step 5.
+// The waves synchronise through progress counters in LDS (one word per wave
+// and kind, written only by that wave) instead of workgroup barriers, so
+// neither role waits for the other's whole step: a producer projects head h
+// (registers only), waits until slot h & 1 is free and stores into it; a
+// consumer waits for that store, attends, and out-projects head h one step
+// later; producers out-project head h two steps later, after projecting the
+// next head (ws_producer / ws_consumer list what each wait protects).  Every
+// wait is bounded (ws_wait).
 //
 // LDS: X (L rows, swizzled as eoff), then per slot Q and K (L rows rounded up
 // to even) and V (32 ceil(NP / 2) rows).  Operand reads of the last position
@@ -59,10 +57,51 @@ constexpr int kWsFTC = 6 - kWsFTP;    // Y feature tiles of a consumer wave
 #endif
 constexpr int kWsPF = ATX_MHA_WS_PF;  // weight k-steps in flight in the projections
 
+// Progress counters, one 32-bit word per wave and kind, each written only by
+// its wave and only ever increased.
+constexpr int kSyncStore = 0;    // [4] producer p: heads stored into a slot
+constexpr int kSyncAttn = 4;     // [4] consumer c: heads attended (O written)
+constexpr int kSyncOutP = 8;     // [4] producer p: heads out-projected
+constexpr int kSyncOutC = 12;    // [4] consumer c: heads out-projected
+constexpr int kSyncXfree = 16;   // [4] producer p: samples whose X it has read for the last time
+constexpr int kSyncXready = 20;  // [4] producer p: samples whose X rows it has written (and normalised)
+constexpr int kSyncWords = 24;
+
 constexpr int ws_lq(int L) { return (L + 1) & ~1; }
 constexpr int ws_lv(int np) { return 32 * ((np + 1) / 2); }
 constexpr size_t ws_slot(int L) { return (size_t)(2 * ws_lq(L) + ws_lv((L + 15) / 16)) * kD * 2; }
-constexpr size_t ws_lds(int L) { return (size_t)L * kWsE * 2 + 2 * ws_slot(L); }
+constexpr size_t ws_lds(int L) { return (size_t)L * kWsE * 2 + 2 * ws_slot(L) + kSyncWords * 4; }
+
+// Publishes count v of this wave: every LDS access the wave issued before
+// (reads included) has completed before the count is visible.
+__device__ inline void ws_post(lds_t* sync, int word, uint32_t v) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    *reinterpret_cast<volatile __attribute__((address_space(3))) uint32_t*>(sync + 4 * word) = v;
+}
+// Waits until each of the NW (4 or 8) counts from `word` on is >= target;
+// each poll reads them with NW / 4 16-byte LDS reads issued together.
+// Bounded: a wait gives up after kWsSpin polls (about a million cycles, two
+// orders of magnitude above the longest legitimate wait, one role's step),
+// so the kernel ends even if the schedule were wrong -- its results would
+// be, and the parity tests would see it.
+constexpr uint32_t kWsSpin = 1u << 14;
+template <int NW = 4>
+__device__ inline void ws_wait(const lds_t* sync, int word, uint32_t target) {
+    static_assert(NW == 4 || NW == 8, "4 or 8 counters");
+    typedef const volatile __attribute__((address_space(3))) u32x4 vu32x4;
+    vu32x4* w = reinterpret_cast<vu32x4*>(sync + 4 * word);
+    for (uint32_t n = 0; n < kWsSpin; ++n) {
+        const u32x4 a = w[0];
+        uint32_t lo = min(min(a[0], a[1]), min(a[2], a[3]));
+        if constexpr (NW == 8) {
+            const u32x4 b = w[1];
+            lo = min(lo, min(min(b[0], b[1]), min(b[2], b[3])));
+        }
+        if (__builtin_amdgcn_readfirstlane(lo) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");  // no LDS access of the caller moves above the wait
+}
 
 // Producer p, head h: feature tile p of Q_h, K_h and V_h for every position
 // tile, accumulated over the E inputs in 12 k-steps of 32.  The weight rows of
@@ -365,29 +404,6 @@ __device__ __forceinline__ void ws_store(const f32x4 (&acc)[3][NP], lds_t* sq, l
     }
 }
 
-// Residual rows of sample b for ws_store_y, loaded ahead of the
-// out-projection: per pair of tiles and position tile the 16 bytes of x a
-// lane's store covers after the lane swaps, and for an odd last tile its 8.
-template <int FT, int NP>
-struct WsRes {
-    u32x4 pair[FT / 2 > 0 ? FT / 2 : 1][NP];
-    u32x2 odd[NP];
-};
-template <typename T, int FT, int NP>
-__device__ __forceinline__ void ws_load_res(WsRes<FT, NP>& r, const MhaArgs& a, int b, int ft0, int m, int g) {
-    const int L = a.L;
-    const rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + b * a.xsb, (uint32_t)(((L - 1) * a.xss + kWsE) * 2));
-#pragma unroll
-    for (int fp = 0; fp < FT / 2; ++fp)
-#pragma unroll
-        for (int q = 0; q < NP; ++q)
-            r.pair[fp][q] = buf_ld16_keep(rx, (uint32_t)((q * 16 + m) * a.xss + (ft0 + 2 * fp) * 16 + 8 * g) * 2);
-    if constexpr (FT % 2 == 1)
-#pragma unroll
-        for (int q = 0; q < NP; ++q)
-            r.odd[q] = __builtin_amdgcn_raw_buffer_load_b64(rx, (int)((q * 16 + m) * a.xss + (ft0 + FT - 1) * 16 + 4 * g) * 2, 0, 0);
-}
-
 // 16-bit pair w (as the layer rounded it) + residual pair r, rounded again:
 // x + attn(...) of transformer.py:143 in the 16-bit type.
 template <typename T>
@@ -398,21 +414,32 @@ __device__ inline uint32_t add_res2(uint32_t w, uint32_t r) {
 }
 
 // Y feature tiles ft0 .. ft0 + FT - 1 (+ bias) of sample b, rounded once (and,
-// with a residual, added to x and rounded again); rows past L are dropped.
+// with RES, added to x and rounded again); rows past L are dropped.
 // In the MFMA layout a lane holds 4 consecutive features (8 bytes) of one row
 // per tile.  For each pair of tiles, two lane swaps across the 16-lane groups
 // (pairing groups 0,1 with 2,3, then 0 with 1 and 2 with 3) leave lane group
 // g with features 8g .. 8g + 7 of the pair's 32, so each store writes 16
 // bytes per lane and 64 contiguous bytes per row: half the store
-// instructions and write requests of 8-byte stores.
-template <typename T, int FT, int NP>
-__device__ __forceinline__ void ws_store_y(const f32x4 (&yacc)[FT][NP], const MhaArgs& a, int b, int ft0, int m, int g,
-                                           const WsRes<FT, NP>& res) {
+// instructions and write requests of 8-byte stores.  With RES the residual
+// pieces of x the stores cover are loaded one pair of tiles at a time, the
+// next pair's in flight while the current pair is stored (all at once they
+// would not fit in registers beside the accumulators).
+template <typename T, int FT, int NP, bool RES>
+__device__ __forceinline__ void ws_store_y(const f32x4 (&yacc)[FT][NP], const MhaArgs& a, int b, int ft0, int m, int g) {
     using M = Mfma16<T>;
     const int L = a.L;
-    const bool resid = a.residual != 0;
     const rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + b * a.ysb, (uint32_t)(((L - 1) * a.yss + kWsE) * 2));
+    const rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + b * a.xsb, (uint32_t)(((L - 1) * a.xss + kWsE) * 2));
     const T* const bo = static_cast<const T*>(a.bias[3]);
+    constexpr int NPAIR = FT / 2;
+    // Residual pieces of pair fp, position tile q: the 16 bytes a lane stores.
+    const auto res_ld = [&](int fp, int q) {
+        return buf_ld16_keep(rx, (uint32_t)((q * 16 + m) * a.xss + (ft0 + 2 * fp) * 16 + 8 * g) * 2);
+    };
+    u32x4 rcur[NP], rnext[NP];
+    if constexpr (RES && NPAIR > 0)
+#pragma unroll
+        for (int q = 0; q < NP; ++q) rcur[q] = res_ld(0, q);
     // Bias of features 16 (ft0 + f) + 4g .. + 3, read before any store (a
     // wait for the loads would otherwise wait for the stores too).
     f32x4 bv[FT];
@@ -424,7 +451,11 @@ __device__ __forceinline__ void ws_store_y(const f32x4 (&yacc)[FT][NP], const Mh
             for (int i = 0; i < 4; ++i) bv[f][i] = static_cast<float>(bo[(ft0 + f) * 16 + 4 * g + i]);
     }
 #pragma unroll
-    for (int fp = 0; fp < FT / 2; ++fp)
+    for (int fp = 0; fp < NPAIR; ++fp) {
+        if constexpr (RES)
+            if (fp + 1 < NPAIR)
+#pragma unroll
+                for (int q = 0; q < NP; ++q) rnext[q] = res_ld(fp + 1, q);
 #pragma unroll
         for (int q = 0; q < NP; ++q) {
             const f32x4& ya = yacc[2 * fp][q];
@@ -438,22 +469,33 @@ __device__ __forceinline__ void ws_store_y(const f32x4 (&yacc)[FT][NP], const Mh
             lane_swap16(x0, y0);
             lane_swap16(x1, y1);
             u32x4 out = u32x4{x0, x1, y0, y1};
-            if (resid)
+            if constexpr (RES)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) out[i] = add_res2<T>(out[i], res.pair[fp][q][i]);
+                for (int i = 0; i < 4; ++i) out[i] = add_res2<T>(out[i], rcur[q][i]);
             buf_st16_cached(ry, (uint32_t)((q * 16 + m) * a.yss + (ft0 + 2 * fp) * 16 + 8 * g) * 2, out);
         }
-    if constexpr (FT % 2 == 1)  // an odd last tile: 8 bytes per lane
+        if constexpr (RES)
+            if (fp + 1 < NPAIR)
+#pragma unroll
+                for (int q = 0; q < NP; ++q) rcur[q] = rnext[q];
+    }
+    if constexpr (FT % 2 == 1) {  // an odd last tile: 8 bytes per lane
+        u32x2 rodd[NP];
+        if constexpr (RES)
+#pragma unroll
+            for (int q = 0; q < NP; ++q)
+                rodd[q] = __builtin_amdgcn_raw_buffer_load_b64(rx, (int)((q * 16 + m) * a.xss + (ft0 + FT - 1) * 16 + 4 * g) * 2, 0, 0);
 #pragma unroll
         for (int q = 0; q < NP; ++q) {
             const f32x4& y = yacc[FT - 1][q];
             const f32x4& bb = bv[FT - 1];
             u32x2 out = u32x2{M::pack2(y[0] + bb[0], y[1] + bb[1]), M::pack2(y[2] + bb[2], y[3] + bb[3])};
-            if (resid)
+            if constexpr (RES)
 #pragma unroll
-                for (int i = 0; i < 2; ++i) out[i] = add_res2<T>(out[i], res.odd[q][i]);
+                for (int i = 0; i < 2; ++i) out[i] = add_res2<T>(out[i], rodd[q][i]);
             buf_st8_cached(ry, (uint32_t)((q * 16 + m) * a.yss + (ft0 + FT - 1) * 16 + 4 * g) * 2, out);
         }
+    }
 }
 
 // X rows of sample b into LDS (swizzled), by NTHR threads (thread index t).
@@ -610,35 +652,27 @@ __device__ __forceinline__ void ws_load_wo(u32x4 (&wo)[2][FT], rsrc_t rwo, int f
 struct WsCtx {
     lds_t* sx0;  // X
     lds_t* ss0;  // slot 0 (slot 1 follows at +slot)
+    lds_t* sync; // progress counters (after slot 1)
     int slot;    // bytes per slot
     int LQ;      // Q / K rows per slot
     int lane;
     int batch;
 };
 
-// Part 1 of step s (shared by both roles): the out-projection of head s - 2,
-// or at step 0 of every sample but the first that of the previous sample's
-// last head, followed by the previous sample's Y store.
-template <typename T, int FT, int NP>
-__device__ __forceinline__ void ws_out_proj(f32x4 (&yacc)[FT][NP], const u32x4 (&wo)[2][FT], const WsCtx& c, const MhaArgs& a,
-                                            int b, int s, int ft0, int m, int g) {
-    if (s >= 2 || (s == 0 && b != (int)blockIdx.x)) {
-        const int hh = s >= 2 ? s - 2 : kWsH - 1;
-        WsRes<FT, NP> res;  // the previous sample's residual rows, in flight during the out-projection
-        if (s == 0 && a.residual) ws_load_res<T, FT, NP>(res, a, b - (int)gridDim.x, ft0, m, g);
-        out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + (hh & 1) * c.slot, m, g);
-        if (s == 0) {
-            ws_store_y<T, FT, NP>(yacc, a, b - (int)gridDim.x, ft0, m, g, res);
-#pragma unroll
-            for (int f = 0; f < FT; ++f)
-#pragma unroll
-                for (int q = 0; q < NP; ++q) yacc[f][q] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-}
-
-// Producer wave p (0..3): owns Y feature tiles kWsFTP p .. kWsFTP p + kWsFTP - 1.
-template <typename T, int NP, bool PK>
+// ---------------------------------------------------------------------------
+// The two roles.  Heads are numbered t = 6 i + s over the workgroup's samples
+// i; head t uses slot t & 1.  What each wait protects:
+//  * a producer stores head t into slot t & 1 once all eight waves have
+//    out-projected head t - 2 from it (which each does only after every
+//    consumer has attended head t - 2 there);
+//  * a consumer attends head t once every producer has stored it;
+//  * every wave out-projects head h once every consumer has attended it;
+//  * a producer overwrites X with the next sample's rows once every producer
+//    has projected the last head from it, and projects the next sample once
+//    every producer has written (and normalised) its rows.
+// Producers out-project head t - 2 before projecting head t, consumers head
+// t - 1 right after attending it; consumers never read X.
+template <typename T, int NP, bool PK, bool RES>
 __device__ __forceinline__ void ws_producer(const WsCtx& c, const MhaArgs& a, const rsrc_t (&rw)[4], int p) {
     constexpr int FT = kWsFTP;
     const int ft0 = FT * p;
@@ -649,74 +683,89 @@ __device__ __forceinline__ void ws_producer(const WsCtx& c, const MhaArgs& a, co
 #pragma unroll
         for (int q = 0; q < NP; ++q) yacc[f][q] = f32x4{0.f, 0.f, 0.f, 0.f};
     u32x4 wo[2][FT];
-    // Steps 0 .. 4 in a loop; the last head's projection (step 5) and step 6
-    // are written out, so that the next sample's X, loaded at the end of
-    // step 5, is live only across them.
-    const auto project = [&](int b, int s, int m, int g, f32x4 (&acc)[3][NP]) {
-        ws_out_proj<T, FT, NP>(yacc, wo, c, a, b, s, ft0, m, g);
-        ws_project<T, NP, PK>(lds_opaque(c.sx0), m, g, rw, wtile_off<kWsE, PK>(s * 4 + p, m, g), acc);
-        // (Unconditional, so `wo` is dead during the projections: at step 0
-        // this loads head 0's operands, which nothing uses.)
-        ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, s > 0 ? s - 1 : 0);
+    // Out-projection of head t - 2 (at s = 1 the previous sample's last head,
+    // then that sample's Y).
+    const auto out_proj = [&](int b, int s, uint32_t t, int m, int g) {
+        ws_wait(c.sync, kSyncAttn, t - 1);
+        out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + ((t - 2) & 1) * c.slot, m, g);
+        ws_post(c.sync, kSyncOutP + p, t - 1);
+        if (s == 1) {
+            ws_store_y<T, FT, NP, RES>(yacc, a, b - grid, ft0, m, g);
+#pragma unroll
+            for (int f = 0; f < FT; ++f)
+#pragma unroll
+                for (int q = 0; q < NP; ++q) yacc[f][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
     };
-    const auto store = [&](int s, int m, int g, const f32x4 (&acc)[3][NP]) {
-        lds_t* const sq = lds_opaque(c.ss0) + (s & 1) * c.slot;
+    // Head t into slot t & 1 once all eight waves have out-projected head t - 2.
+    const auto store = [&](int s, uint32_t t, int m, int g, const f32x4 (&acc)[3][NP]) {
+        if (t >= 2) ws_wait<8>(c.sync, kSyncOutP, t - 1);  // kSyncOutP and kSyncOutC
+        lds_t* const sq = lds_opaque(c.ss0) + (t & 1) * c.slot;
         ws_store<T, NP>(acc, sq, sq + c.LQ * kD * 2, sq + 2 * c.LQ * kD * 2, a.bias, s, p, opaque_s(a.L), m, g);
+        ws_post(c.sync, kSyncStore + p, t + 1);
     };
-    for (int b = blockIdx.x; b < c.batch; b += grid) {
-        for (int s = 0; s < kWsH - 1; ++s) {
-            // Per-lane offsets are re-derived every step from an opaque copy:
-            // hoisted out of the loops, the compiler would keep dozens of
-            // them live throughout and spill.
+    uint32_t t = 0;  // head number
+    uint32_t i = 0;  // sample number
+    for (int b = blockIdx.x; b < c.batch; b += grid, ++i) {
+        for (int s = 0; s < kWsH - 1; ++s, ++t) {
             const int ln = opaque_v(c.lane);
             const int m = ln & 15, g = ln >> 4;
+            if (t >= 2) out_proj(b, s, t, m, g);
+            if (s == 0 && i > 0) ws_wait(c.sync, kSyncXready, i);  // every producer's rows of this sample's X
             f32x4 acc[3][NP];
-            project(b, s, m, g, acc);
-            __syncthreads();
-            store(s, m, g, acc);
-            __syncthreads();
+            ws_project<T, NP, PK>(lds_opaque(c.sx0), m, g, rw, wtile_off<kWsE, PK>(s * 4 + p, m, g), acc);
+            // (Head t - 1's operands for the next out-projection; at t = 0
+            // head 5's, which nothing uses.)
+            ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, s > 0 ? s - 1 : kWsH - 1);
+            store(s, t, m, g, acc);
         }
+        // The last head, then the next sample's X.
         const int ln = opaque_v(c.lane);
         const int m = ln & 15, g = ln >> 4;
         const bool more = b + grid < c.batch;
-        // (After the last sample this re-reads its own X, unused: the issue
-        // stays branch-free.)
+        out_proj(b, kWsH - 1, t, m, g);
         u32x4 xv[ws_xu<NP>()];
         {
             f32x4 acc[3][NP];
-            project(b, kWsH - 1, m, g, acc);
-            // (Part of the loads here; the rest once acc is stored.)
+            ws_project<T, NP, PK>(lds_opaque(c.sx0), m, g, rw, wtile_off<kWsE, PK>((kWsH - 1) * 4 + p, m, g), acc);
+            ws_post(c.sync, kSyncXfree + p, i + 1);
+            ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, kWsH - 2);
+            // (Part of the loads here; the rest once acc is stored.  After
+            // the last sample this re-reads its own X, unused: the issue
+            // stays branch-free.)
             __builtin_amdgcn_sched_barrier(0);
             ws_x_issue<T, ws_xu<NP>(), 0, kWsXEarly>(xv, a, more ? b + grid : b, p, ln);
-            __syncthreads();
-            store(kWsH - 1, m, g, acc);
-            __syncthreads();
+            store(kWsH - 1, t, m, g, acc);
         }
+        ++t;
         __builtin_amdgcn_sched_barrier(0);
         ws_x_issue<T, ws_xu<NP>(), kWsXEarly, ws_xu<NP>()>(xv, a, more ? b + grid : b, p, ln);
         __builtin_amdgcn_sched_barrier(0);
-        ws_out_proj<T, FT, NP>(yacc, wo, c, a, b, kWsH, ft0, m, g);
         if (more) {
+            ws_wait(c.sync, kSyncXfree, i + 1);  // every producer is done with this sample's X
             ws_x_commit<ws_xu<NP>()>(xv, lds_opaque(c.sx0), a.L, p, ln);
             if (a.ln_w) {
                 wave_lds_handoff();  // the wave reads back the rows it wrote
                 ws_layernorm_rows<T>(lds_opaque(c.sx0), a, p, 4, c.lane);
             }
         }
-        ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, kWsH - 1);
-        __syncthreads();
+        ws_post(c.sync, kSyncXready + p, i + 1);
     }
+    // Heads T - 2 and T - 1 of the last sample, then its Y.
     const int m = c.lane & 15, g = c.lane >> 4;
     const int last = blockIdx.x + ((c.batch - 1 - (int)blockIdx.x) / grid) * grid;
-    WsRes<FT, NP> res;
-    if (a.residual) ws_load_res<T, FT, NP>(res, a, last, ft0, m, g);
-    out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + ((kWsH - 1) & 1) * c.slot, m, g);
-    ws_store_y<T, FT, NP>(yacc, a, last, ft0, m, g, res);
+    ws_wait(c.sync, kSyncAttn, t - 1);
+    out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + ((t - 2) & 1) * c.slot, m, g);
+    ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, kWsH - 1);
+    ws_wait(c.sync, kSyncAttn, t);
+    out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + ((t - 1) & 1) * c.slot, m, g);
+    ws_store_y<T, FT, NP, RES>(yacc, a, last, ft0, m, g);
 }
 
-// Consumer wave 4 + cq (cq 0..3): query tiles cq and cq + 4; owns the kWsFTC
-// Y feature tiles from 4 kWsFTP + kWsFTC cq on.
-template <typename T, int NP, bool CAUSAL, bool PK>
+// Consumer wave 4 + cq, 7 steps per sample: attention of head s - 1 at step
+// s = 1 .. 6, out-projection of head s - 2 at step s and of the previous
+// sample's last head (then that sample's Y) at step 0.
+template <typename T, int NP, bool CAUSAL, bool PK, bool RES>
 __device__ __forceinline__ void ws_consumer(const WsCtx& c, const MhaArgs& a, const rsrc_t (&rw)[4], int cq) {
     constexpr int FT = kWsFTC;
     const int ft0 = 4 * kWsFTP + FT * cq;
@@ -727,14 +776,29 @@ __device__ __forceinline__ void ws_consumer(const WsCtx& c, const MhaArgs& a, co
 #pragma unroll
         for (int q = 0; q < NP; ++q) yacc[f][q] = f32x4{0.f, 0.f, 0.f, 0.f};
     u32x4 wo[2][FT];
-    for (int b = blockIdx.x; b < c.batch; b += grid) {
+    uint32_t t0 = 0;  // number of this sample's head 0
+    for (int b = blockIdx.x; b < c.batch; b += grid, t0 += kWsH) {
         for (int s = 0; s <= kWsH; ++s) {
             const int ln = opaque_v(c.lane);
             const int m = ln & 15, g = ln >> 4;
-            ws_out_proj<T, FT, NP>(yacc, wo, c, a, b, s, ft0, m, g);
+            if (s >= 2 || (s == 0 && t0 > 0)) {
+                const uint32_t h = s >= 2 ? t0 + s - 2 : t0 - 1;  // head to out-project
+                ws_wait(c.sync, kSyncAttn, h + 1);
+                out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + (h & 1) * c.slot, m, g);
+                ws_post(c.sync, kSyncOutC + cq, h + 1);
+                if (s == 0) {
+                    ws_store_y<T, FT, NP, RES>(yacc, a, b - grid, ft0, m, g);
+#pragma unroll
+                    for (int f = 0; f < FT; ++f)
+#pragma unroll
+                        for (int q = 0; q < NP; ++q) yacc[f][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
             if (s >= 1) {
+                const uint32_t h = t0 + s - 1;  // head to attend
+                ws_wait(c.sync, kSyncStore, h + 1);
                 const int L = opaque_s(a.L);
-                lds_t* const sq = lds_opaque(c.ss0) + ((s - 1) & 1) * c.slot;
+                lds_t* const sq = lds_opaque(c.ss0) + (h & 1) * c.slot;
                 lds_t* const sk = sq + c.LQ * kD * 2;
                 lds_t* const sv = sk + c.LQ * kD * 2;
                 const auto put = [&](int qt, const u32x4 (&out)[2]) {
@@ -759,21 +823,19 @@ __device__ __forceinline__ void ws_consumer(const WsCtx& c, const MhaArgs& a, co
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
+                ws_post(c.sync, kSyncAttn + cq, h + 1);
             }
             ws_load_wo<FT, PK>(wo, rw[3], ft0, m, g, s > 0 ? s - 1 : 0);
-            __syncthreads();
-            if (s < kWsH) __syncthreads();  // the producers' stores
         }
     }
     const int m = c.lane & 15, g = c.lane >> 4;
     const int last = blockIdx.x + ((c.batch - 1 - (int)blockIdx.x) / grid) * grid;
-    WsRes<FT, NP> res;
-    if (a.residual) ws_load_res<T, FT, NP>(res, a, last, ft0, m, g);
-    out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + ((kWsH - 1) & 1) * c.slot, m, g);
-    ws_store_y<T, FT, NP>(yacc, a, last, ft0, m, g, res);
+    ws_wait(c.sync, kSyncAttn, t0);
+    out_proj_head<T, FT, NP>(yacc, wo, lds_opaque(c.ss0) + ((t0 - 1) & 1) * c.slot, m, g);
+    ws_store_y<T, FT, NP, RES>(yacc, a, last, ft0, m, g);
 }
 
-template <typename T, int NP, bool CAUSAL, bool PK>
+template <typename T, int NP, bool CAUSAL, bool PK, bool RES>
 __global__ __launch_bounds__(kThreads) void mha_ws(MhaArgs a, int batch) {
     constexpr int E = kWsE;
     constexpr int LP = NP * 16;
@@ -790,6 +852,8 @@ __global__ __launch_bounds__(kThreads) void mha_ws(MhaArgs a, int batch) {
     c.slot = (2 * c.LQ + LV) * kD * 2;
     c.sx0 = lds_base();
     c.ss0 = c.sx0 + a.L * E * 2;
+    c.sync = c.ss0 + 2 * c.slot;
+    if (tid < kSyncWords) lds_st4(c.sync + 4 * tid, 0u);  // (visible after the first barrier)
 
     rsrc_t rw[4];
 #pragma unroll
@@ -807,13 +871,13 @@ __global__ __launch_bounds__(kThreads) void mha_ws(MhaArgs a, int batch) {
         __syncthreads();
     }
 
-    // The two roles run separate loops with the same barriers in the same
-    // order (the branch is uniform over each wave), each with its own
-    // registers.
+    // The two roles run separate loops (the branch is uniform over each
+    // wave), each with its own registers; after the prologue's barriers they
+    // meet only through the progress counters.
     if (wave < 4)
-        ws_producer<T, NP, PK>(c, a, rw, wave);
+        ws_producer<T, NP, PK, RES>(c, a, rw, wave);
     else
-        ws_consumer<T, NP, CAUSAL, PK>(c, a, rw, wave - 4);
+        ws_consumer<T, NP, CAUSAL, PK, RES>(c, a, rw, wave - 4);
 }
 
 template <typename K>
@@ -825,14 +889,22 @@ int launch_ws(K kernel, int grid, int batch, size_t lds, hipStream_t st, const M
     return ATX_OK;
 }
 
-template <typename T, bool CAUSAL, bool PK>
-int ws_np(int np, int grid, int batch, size_t lds, hipStream_t st, const MhaArgs& a) {
+template <typename T, bool CAUSAL, bool PK, bool RES>
+int ws_np_res(int np, int grid, int batch, size_t lds, hipStream_t st, const MhaArgs& a) {
     switch (np) {
-        case 5: return launch_ws(mha_ws<T, 5, CAUSAL, PK>, grid, batch, lds, st, a);
-        case 6: return launch_ws(mha_ws<T, 6, CAUSAL, PK>, grid, batch, lds, st, a);
-        case 7: return launch_ws(mha_ws<T, 7, CAUSAL, PK>, grid, batch, lds, st, a);
+        case 5: return launch_ws(mha_ws<T, 5, CAUSAL, PK, RES>, grid, batch, lds, st, a);
+        case 6: return launch_ws(mha_ws<T, 6, CAUSAL, PK, RES>, grid, batch, lds, st, a);
+        case 7: return launch_ws(mha_ws<T, 7, CAUSAL, PK, RES>, grid, batch, lds, st, a);
         default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_mha_fwd (persistent form): %d position tiles", np);
     }
+}
+
+// (The residual add is a template parameter: its loads would otherwise take
+// registers in the kernels without it.)
+template <typename T, bool CAUSAL, bool PK>
+int ws_np(int np, int grid, int batch, size_t lds, hipStream_t st, const MhaArgs& a) {
+    return a.residual ? ws_np_res<T, CAUSAL, PK, true>(np, grid, batch, lds, st, a)
+                      : ws_np_res<T, CAUSAL, PK, false>(np, grid, batch, lds, st, a);
 }
 
 constexpr int kMaxDevices = 64;
