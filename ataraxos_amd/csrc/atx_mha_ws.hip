@@ -47,11 +47,13 @@ namespace {
 
 constexpr int kWsH = 6;
 constexpr int kWsE = kWsH * kD;
-#ifndef ATX_MHA_WS_FTP
-#define ATX_MHA_WS_FTP 2
-#endif
-constexpr int kWsFTP = ATX_MHA_WS_FTP;  // Y feature tiles of a producer wave
-constexpr int kWsFTC = 6 - kWsFTP;    // Y feature tiles of a consumer wave
+// Y feature tiles of a producer wave (of the 24: the consumers hold the rest,
+// 6 - ws_ftp each).  Measured at C3: 3 / 3 is 1.8 % faster than 2 / 4 (the
+// consumers' attention is the longer chain); with the residual add, or with
+// weights in the nn.Linear order (wider weight addressing), the 3 / 3 split
+// spills, so those kernels keep 2 / 4.
+template <bool RES, bool PK>
+constexpr int ws_ftp() { return (PK && !RES) ? 3 : 2; }
 #ifndef ATX_MHA_WS_PF
 #define ATX_MHA_WS_PF 2
 #endif
@@ -85,6 +87,9 @@ __device__ inline void ws_post(lds_t* sync, int word, uint32_t v) {
 // so the kernel ends even if the schedule were wrong -- its results would
 // be, and the parity tests would see it.
 constexpr uint32_t kWsSpin = 1u << 14;
+#ifndef ATX_MHA_WS_SLEEP
+#define ATX_MHA_WS_SLEEP 1  // s_sleep argument between polls (units of 64 cycles)
+#endif
 template <int NW = 4>
 __device__ inline void ws_wait(const lds_t* sync, int word, uint32_t target) {
     static_assert(NW == 4 || NW == 8, "4 or 8 counters");
@@ -98,7 +103,7 @@ __device__ inline void ws_wait(const lds_t* sync, int word, uint32_t target) {
             lo = min(lo, min(min(b[0], b[1]), min(b[2], b[3])));
         }
         if (__builtin_amdgcn_readfirstlane(lo) >= target) break;
-        __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_s_sleep(ATX_MHA_WS_SLEEP);
     }
     asm volatile("" ::: "memory");  // no LDS access of the caller moves above the wait
 }
@@ -674,7 +679,7 @@ struct WsCtx {
 // t - 1 right after attending it; consumers never read X.
 template <typename T, int NP, bool PK, bool RES>
 __device__ __forceinline__ void ws_producer(const WsCtx& c, const MhaArgs& a, const rsrc_t (&rw)[4], int p) {
-    constexpr int FT = kWsFTP;
+    constexpr int FT = ws_ftp<RES, PK>();
     const int ft0 = FT * p;
     const int grid = gridDim.x;
     f32x4 yacc[FT][NP];
@@ -767,8 +772,8 @@ __device__ __forceinline__ void ws_producer(const WsCtx& c, const MhaArgs& a, co
 // sample's last head (then that sample's Y) at step 0.
 template <typename T, int NP, bool CAUSAL, bool PK, bool RES>
 __device__ __forceinline__ void ws_consumer(const WsCtx& c, const MhaArgs& a, const rsrc_t (&rw)[4], int cq) {
-    constexpr int FT = kWsFTC;
-    const int ft0 = 4 * kWsFTP + FT * cq;
+    constexpr int FT = 6 - ws_ftp<RES, PK>();
+    const int ft0 = 4 * ws_ftp<RES, PK>() + FT * cq;
     const int grid = gridDim.x;
     f32x4 yacc[FT][NP];
 #pragma unroll
@@ -841,7 +846,7 @@ __global__ __launch_bounds__(kThreads) void mha_ws(MhaArgs a, int batch) {
     constexpr int LP = NP * 16;
     constexpr int LV = ws_lv(NP);
     static_assert(kWaves == 8, "wave roles assume 8 waves");
-    static_assert(4 * kWsFTP + 4 * kWsFTC == E / 16, "Y tiles split over the waves");
+    static_assert(E / 16 == 24, "Y tiles split over the waves: 4 producers and 4 consumers, 6 per pair");
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
