@@ -36,9 +36,14 @@ class KernelMultiheadAttention(nn.MultiheadAttention):
     passes), no mask or the causal mask (``is_causal=True``, the hint
     ``nn.TransformerDecoder`` derives from a ``triu(-inf, 1)`` mask), and a
     bool ``key_padding_mask`` ``[B, S_kv]`` (True = ignore).  Anything else
-    raises on the GPU instead of silently taking another path.  On the CPU,
-    and in training with dropout > 0 (the kernel has no dropout), the forward
-    is ``nn.MultiheadAttention``'s own, as in the reference.
+    raises on the GPU instead of silently taking another path.  In training
+    with ``dropout > 0`` at head_dim 48 or 64 (the Belief decoder's 512 / 8)
+    the kernel drops the attention weights itself, as
+    ``nn.MultiheadAttention`` does (``ops.attention`` with ``dropout_p``: the
+    keep decisions a hash of each weight's index under a seed drawn from
+    torch's default generator per call).  On the CPU, and in training with
+    dropout at other head sizes, the forward is ``nn.MultiheadAttention``'s
+    own, as in the reference.
 
     Self-attention (``query``, ``key`` and ``value`` the same tensor, as
     ``TransformerDecoderLayer`` calls it) without a key padding mask and
@@ -62,7 +67,8 @@ class KernelMultiheadAttention(nn.MultiheadAttention):
         average_attn_weights: bool = True,
         is_causal: bool = False,
     ) -> tuple[torch.Tensor, torch.Tensor | None]:
-        if not query.is_cuda or (self.training and self.dropout > 0.0):
+        drop = self.dropout if (self.training and self.dropout > 0.0) else 0.0
+        if not query.is_cuda or (drop > 0.0 and self.embed_dim // self.num_heads not in ops.DROPOUT_HEAD_DIMS):
             return super().forward(
                 query, key, value, key_padding_mask=key_padding_mask, need_weights=need_weights,
                 attn_mask=attn_mask, average_attn_weights=average_attn_weights, is_causal=is_causal,
@@ -89,7 +95,7 @@ class KernelMultiheadAttention(nn.MultiheadAttention):
         b_q = b_k = b_v = None
         if self.in_proj_bias is not None:
             b_q, b_k, b_v = self.in_proj_bias.chunk(3)
-        if self_attention and key_padding_mask is None and self._fused_ok(query):
+        if self_attention and key_padding_mask is None and drop == 0.0 and self._fused_ok(query):
             assert self.in_proj_weight is not None
             ws = (w_q, w_k, w_v, self.out_proj.weight)
             out = ops.mha_forward(
@@ -101,7 +107,7 @@ class KernelMultiheadAttention(nn.MultiheadAttention):
         q = F.linear(query, w_q, b_q).view(b, sq, h, d)
         k = F.linear(key, w_k, b_k).view(b, skv, h, d)
         v = F.linear(value, w_v, b_v).view(b, skv, h, d)
-        o = ops.attention(q, k, v, causal=is_causal, key_padding_mask=key_padding_mask)
+        o = ops.attention(q, k, v, causal=is_causal, key_padding_mask=key_padding_mask, dropout_p=drop)
         out = self.out_proj(o.reshape(b, sq, e))
         if not self.batch_first:
             out = out.transpose(0, 1)

@@ -130,3 +130,48 @@ def test_decoder_self_attention_fused_sequence_first(cuda):
         ys, _ = ms(xs, xs, xs, need_weights=False)
     assert ys.shape == (48, 5, 384)
     assert torch.equal(ys.transpose(0, 1), yb)
+
+
+def test_decoder_attention_dropout_in_the_kernel(cuda):
+    """Training with the Belief decoder's dropout 0.2 (512 / 8 = head_dim 64):
+    the converted cross-attention drops weights in the kernel; its output is
+    nn.MultiheadAttention's math with the kernel's mask made explicit (fp32),
+    repeatable under the same torch seed, and differentiable."""
+    from ataraxos_amd import ops
+
+    _announce("decoder cross-attention with dropout 0.2 in training")
+    torch.manual_seed(0)
+    m = use_hip_attention(torch.nn.MultiheadAttention(512, 8, dropout=0.2, batch_first=True)).to(cuda).train()
+    b, sq, skv = 4, 40, 100
+    q = torch.randn(b, sq, 512, device=cuda, requires_grad=True)
+    kv = torch.randn(b, skv, 512, device=cuda)
+    pad = torch.rand(b, skv, device=cuda) < 0.3
+    pad[:, 0] = False
+    torch.manual_seed(7)
+    seed = ops.new_dropout_seed()
+    torch.manual_seed(7)
+    out, _ = m(q, kv, kv, key_padding_mask=pad, need_weights=False)
+    torch.manual_seed(7)
+    again, _ = m(q, kv, kv, key_padding_mask=pad, need_weights=False)
+    assert torch.equal(out, again)
+    # nn.MultiheadAttention's math with the kernel's keep decisions
+    w_q, w_k, w_v = m.in_proj_weight.chunk(3)
+    b_q, b_k, b_v = m.in_proj_bias.chunk(3)
+    qh = torch.nn.functional.linear(q, w_q, b_q).view(b, sq, 8, 64).transpose(1, 2)
+    kh = torch.nn.functional.linear(kv, w_k, b_k).view(b, skv, 8, 64).transpose(1, 2)
+    vh = torch.nn.functional.linear(kv, w_v, b_v).view(b, skv, 8, 64).transpose(1, 2)
+    s = torch.matmul(qh, kh.transpose(-1, -2).contiguous()) / 8.0
+    s = s.masked_fill(pad[:, None, None, :], float("-inf"))
+    keep = ops.dropout_mask(b, 8, sq, skv, 0.2, seed, device=cuda).float()
+    scale = 1.0 / (1.0 - torch.tensor(0.2, dtype=torch.float32).item())
+    p = torch.softmax(s, dim=-1) * keep * scale
+    want = m.out_proj(torch.matmul(p, vh).transpose(1, 2).reshape(b, sq, 512))
+    assert _rel(out, want) <= 1e-5
+    out.sum().backward()
+    assert q.grad is not None and torch.isfinite(q.grad).all()
+    # eval: no dropout, deterministic without a seed
+    m.eval()
+    with torch.no_grad():
+        e1, _ = m(q, kv, kv, key_padding_mask=pad, need_weights=False)
+        e2, _ = m(q, kv, kv, key_padding_mask=pad, need_weights=False)
+    assert torch.equal(e1, e2)
