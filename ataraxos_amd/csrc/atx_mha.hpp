@@ -23,6 +23,7 @@ struct MhaArgs {
     const void* ln_b;  // pre-LN bias [E] (NULL: zero)
     float ln_eps;
     int residual;      // 1: y = x + layer output
+    int ws_spin;       // atx_mha_ws.hip: polls before a wait gives up (set by mha_ws_launch)
 };
 
 namespace {

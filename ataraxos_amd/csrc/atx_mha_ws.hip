@@ -38,6 +38,7 @@
 // MFMA output column depends only on its own position's operand column, so
 // the values read past a buffer (even non-finite ones) stay in those columns.
 #include <mutex>
+#include <stdlib.h>
 
 #include "atx_mha.hpp"
 
@@ -67,7 +68,9 @@ constexpr int kSyncOutP = 8;     // [4] producer p: heads out-projected
 constexpr int kSyncOutC = 12;    // [4] consumer c: heads out-projected
 constexpr int kSyncXfree = 16;   // [4] producer p: samples whose X it has read for the last time
 constexpr int kSyncXready = 20;  // [4] producer p: samples whose X rows it has written (and normalised)
-constexpr int kSyncWords = 24;
+constexpr int kSyncAbort = 24;   // nonzero once any wait gave up (see ws_wait)
+constexpr int kSyncSpin = 25;    // polls before a wait gives up (MhaArgs::ws_spin)
+constexpr int kSyncWords = 28;
 
 constexpr int ws_lq(int L) { return (L + 1) & ~1; }
 constexpr int ws_lv(int np) { return 32 * ((np + 1) / 2); }
@@ -84,9 +87,14 @@ __device__ inline void ws_post(lds_t* sync, int word, uint32_t v) {
 // each poll reads them with NW / 4 16-byte LDS reads issued together.
 // Bounded: a wait gives up after kWsSpin polls (about a million cycles, two
 // orders of magnitude above the longest legitimate wait, one role's step),
-// so the kernel ends even if the schedule were wrong -- its results would
-// be, and the parity tests would see it.
-constexpr uint32_t kWsSpin = 1u << 14;
+// so the kernel ends even if the schedule were wrong.  The limit sits in LDS
+// word kSyncSpin, read only once a first poll has failed (a kernel-long
+// register for it costs the MFMA loops spills, and a read on every entry
+// costs a satisfied wait its latency).  A wait that gives up sets the
+// workgroup's abort word, and the workgroup then overwrites all of
+// its samples' Y with NaN before it ends (mha_ws): a broken schedule shows
+// as NaN output, never as plausible wrong numbers.
+constexpr uint32_t kWsSpin = 1u << 14;  // (ATX_MHA_WS_SPIN overrides it, for the tests of this path)
 #ifndef ATX_MHA_WS_SLEEP
 #define ATX_MHA_WS_SLEEP 1  // s_sleep argument between polls (units of 64 cycles)
 #endif
@@ -95,7 +103,8 @@ __device__ inline void ws_wait(const lds_t* sync, int word, uint32_t target) {
     static_assert(NW == 4 || NW == 8, "4 or 8 counters");
     typedef const volatile __attribute__((address_space(3))) u32x4 vu32x4;
     vu32x4* w = reinterpret_cast<vu32x4*>(sync + 4 * word);
-    for (uint32_t n = 0; n < kWsSpin; ++n) {
+    uint32_t spin = 0;
+    for (uint32_t n = 1;; ++n) {
         const u32x4 a = w[0];
         uint32_t lo = min(min(a[0], a[1]), min(a[2], a[3]));
         if constexpr (NW == 8) {
@@ -103,6 +112,11 @@ __device__ inline void ws_wait(const lds_t* sync, int word, uint32_t target) {
             lo = min(lo, min(min(b[0], b[1]), min(b[2], b[3])));
         }
         if (__builtin_amdgcn_readfirstlane(lo) >= target) break;
+        if (n == 1) spin = __builtin_amdgcn_readfirstlane(lds_ld4(sync + 4 * kSyncSpin));  // (off the fast path)
+        if (n >= spin) {
+            *reinterpret_cast<volatile __attribute__((address_space(3))) uint32_t*>(const_cast<lds_t*>(sync) + 4 * kSyncAbort) = 1u;
+            break;
+        }
         __builtin_amdgcn_s_sleep(ATX_MHA_WS_SLEEP);
     }
     asm volatile("" ::: "memory");  // no LDS access of the caller moves above the wait
@@ -840,6 +854,21 @@ __device__ __forceinline__ void ws_consumer(const WsCtx& c, const MhaArgs& a, co
     ws_store_y<T, FT, NP, RES>(yacc, a, last, ft0, m, g);
 }
 
+// Y of every sample of this workgroup set to NaN (after a wait gave up).
+template <typename T>
+__device__ void ws_poison_y(const MhaArgs& a, int batch, int tid) {
+    using M = Mfma16<T>;
+    constexpr int YC = kWsE / 8;  // 16-byte chunks per row
+    const uint32_t nan2 = M::pack2(__builtin_nanf(""), __builtin_nanf(""));
+    for (int b = blockIdx.x; b < batch; b += gridDim.x) {
+        const rsrc_t ry = make_rsrc(static_cast<const T*>(a.y) + b * a.ysb, (uint32_t)(((a.L - 1) * a.yss + kWsE) * 2));
+        for (int idx = tid; idx < a.L * YC; idx += kThreads) {
+            const int r = idx / YC, c = idx - (idx / YC) * YC;
+            buf_st16_cached(ry, (uint32_t)(r * a.yss + c * 8) * 2, u32x4{nan2, nan2, nan2, nan2});
+        }
+    }
+}
+
 template <typename T, int NP, bool CAUSAL, bool PK, bool RES>
 __global__ __launch_bounds__(kThreads) void mha_ws(MhaArgs a, int batch) {
     constexpr int E = kWsE;
@@ -858,7 +887,7 @@ __global__ __launch_bounds__(kThreads) void mha_ws(MhaArgs a, int batch) {
     c.sx0 = lds_base();
     c.ss0 = c.sx0 + a.L * E * 2;
     c.sync = c.ss0 + 2 * c.slot;
-    if (tid < kSyncWords) lds_st4(c.sync + 4 * tid, 0u);  // (visible after the first barrier)
+    if (tid < kSyncWords) lds_st4(c.sync + 4 * tid, tid == kSyncSpin ? (uint32_t)a.ws_spin : 0u);  // (visible after the first barrier)
 
     rsrc_t rw[4];
 #pragma unroll
@@ -883,6 +912,10 @@ __global__ __launch_bounds__(kThreads) void mha_ws(MhaArgs a, int batch) {
         ws_producer<T, NP, PK, RES>(c, a, rw, wave);
     else
         ws_consumer<T, NP, CAUSAL, PK, RES>(c, a, rw, wave - 4);
+    // Every wave's Y stores complete before any poison store is issued.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (__builtin_amdgcn_readfirstlane(lds_ld4(c.sync + 4 * kSyncAbort)) != 0) ws_poison_y<T>(a, batch, tid);
 }
 
 template <typename K>
@@ -942,7 +975,13 @@ size_t mha_ws_lds_bytes(int E, int L) {
     return lds <= 160 * 1024 ? lds : 0;
 }
 
-int mha_ws_launch(int L, bool causal, bool bf16, bool packed, int batch, size_t lds, hipStream_t st, const MhaArgs& a) {
+int mha_ws_launch(int L, bool causal, bool bf16, bool packed, int batch, size_t lds, hipStream_t st, const MhaArgs& args) {
+    MhaArgs a = args;
+    a.ws_spin = (int)kWsSpin;
+    if (const char* env = getenv("ATX_MHA_WS_SPIN")) {  // tests: force the give-up path
+        const long v = strtol(env, nullptr, 10);
+        if (v >= 1 && v < (long)kWsSpin) a.ws_spin = (int)v;
+    }
     int ncu = 0;
     if (const int rc = cu_count(&ncu)) return rc;
     const int grid = batch < ncu ? batch : ncu;

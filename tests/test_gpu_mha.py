@@ -459,3 +459,29 @@ def test_head_dim_48_full_batch_sampled_rows(cuda):
     err = float(np.max(np.abs(got - ref)))
     assert np.isfinite(got).all()
     assert err <= 2e-2, err
+
+
+def test_persistent_layer_that_gives_up_a_wait_writes_nan(cuda, monkeypatch):
+    """The persistent layer's waves wait on each other through bounded polls.
+    If a wait ever gave up (a broken schedule), the workgroup overwrites its
+    samples' Y with NaN instead of leaving plausible wrong numbers.  Forced
+    here from the host: ATX_MHA_WS_SPIN=1 lets every wait poll once, so the
+    consumers' first wait (for the producers' first store) gives up; every
+    wave still runs to its end.  512 samples make workgroups run two each;
+    rows past the sequence stay unwritten."""
+    b, l, e = 512, 100, 384
+    _announce("mha persistent form, waits limited to one poll")
+    monkeypatch.setenv("ATX_MHA_PERSISTENT", "1")
+    x = randn((b, l, e), 77, torch.bfloat16).to(cuda)
+    ws, _ = layer(e, torch.bfloat16, 78, False)
+    pk = [ops.mha_pack_weight(w.to(cuda)) for w in ws]
+    good = ops.mha_forward(x, *pk, num_heads=6, packed=True)
+    monkeypatch.setenv("ATX_MHA_WS_SPIN", "1")
+    guard = torch.full((b, l + 2, e), 3.0, dtype=torch.bfloat16, device=cuda)
+    ops.mha_forward(x, *pk, num_heads=6, packed=True, out=guard[:, :l])
+    torch.cuda.synchronize()
+    assert torch.isnan(guard[:, :l].float()).all()
+    assert (guard[:, l:] == 3.0).all(), "rows past the sequence were written"
+    monkeypatch.delenv("ATX_MHA_WS_SPIN")
+    again = ops.mha_forward(x, *pk, num_heads=6, packed=True)
+    assert torch.isfinite(good.float()).all() and torch.equal(good, again)
