@@ -309,6 +309,7 @@ __device__ inline uint32_t lds_ld4(const lds_t* p) { return *reinterpret_cast<co
 __device__ inline void lds_st4(lds_t* p, uint32_t v) { *reinterpret_cast<__attribute__((address_space(3))) uint32_t*>(p) = v; }
 __device__ inline uint32_t lds_ld1(const lds_t* p) { return *reinterpret_cast<const __attribute__((address_space(3))) uint8_t*>(p); }
 __device__ inline void lds_st1(lds_t* p, uint32_t v) { *reinterpret_cast<__attribute__((address_space(3))) uint8_t*>(p) = (uint8_t)v; }
+__device__ inline void lds_st2(lds_t* p, uint32_t v) { *reinterpret_cast<__attribute__((address_space(3))) uint16_t*>(p) = (uint16_t)v; }
 
 // 16-byte global load / store through the vector memory path.
 __device__ inline u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }

@@ -90,13 +90,45 @@ void kq_bwd_16bit(KqBwdArgs a) {
     const int b = blockIdx.x;
     const int S = a.S;
 
-    lds_t* const sg_ = sg;
-    kq_bwd_dl<RP, PROBS>(a, b, sred, [&](int i, int c, const float (&dl)[8]) {
-        lds_st16(sg_ + chunk_off_w<RP>(i, c), u32x4{M::pack2(dl[0], dl[1]), M::pack2(dl[2], dl[3]),
-                                                       M::pack2(dl[4], dl[5]), M::pack2(dl[6], dl[7])});
-    });
     const rsrc_t rq = make_rsrc(static_cast<const T*>(a.q) + b * a.qsb, (uint32_t)(((S - 1) * a.qss + a.Dfull) * 2));
     const rsrc_t rk = make_rsrc(static_cast<const T*>(a.k) + b * a.ksb, (uint32_t)(((S - 1) * a.kss + a.Dfull) * 2));
+    // Q and K rows of a column slice, in registers between the loads and the
+    // LDS stores (rows past S read 0): the first slice's loads go out before
+    // phase 1, each next slice's before the current slice's products, so the
+    // loads wait under other work.
+    constexpr int QKU = (RP * CH + kThreads - 1) / kThreads;  // chunks per thread and tensor
+    u32x4 qn[QKU], kn[QKU];
+    auto issue_qk = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < QKU; ++u) {
+            const int idx = tid + u * kThreads;
+            const int r = idx / CH, c = idx - (idx / CH) * CH;
+            const bool in = idx < RP * CH;
+            qn[u] = buf_ld16(rq, in ? (uint32_t)(r * a.qss + c0 + c * 8) * 2 : kOut);
+            kn[u] = buf_ld16(rk, in ? (uint32_t)(r * a.kss + c0 + c * 8) * 2 : kOut);
+        }
+    };
+    auto commit_qk = [&]() {
+#pragma unroll
+        for (int u = 0; u < QKU; ++u) {
+            const int idx = tid + u * kThreads;
+            const int r = idx / CH, c = idx - (idx / CH) * CH;
+            if (idx < RP * CH) {
+                lds_st16(sq + chunk_off_w<D>(r, c), qn[u]);
+                lds_st16(sk + chunk_off_w<D>(r, c), kn[u]);
+            }
+        }
+    };
+    issue_qk(0);
+
+    lds_t* const sg_ = sg;
+    kq_bwd_dl<RP, PROBS>(
+        a, b, sred,
+        [&](int i, int c, const float (&dl)[8]) {
+            lds_st16(sg_ + chunk_off_w<RP>(i, c), u32x4{M::pack2(dl[0], dl[1]), M::pack2(dl[2], dl[3]),
+                                                           M::pack2(dl[4], dl[5]), M::pack2(dl[6], dl[7])});
+        },
+        [&](int i, int j, float v) { lds_st2(sg_ + quad_off_w<RP>(i, j), M::pack2(v, 0.f)); });
 
     // ---- phase 2: dq^T = K^T dL^T, dk^T = Q^T dL --------------------------------
     // Transposing reads of Q / K: input lane a4 + 4t of a 16-lane group points
@@ -131,13 +163,9 @@ void kq_bwd_16bit(KqBwdArgs a) {
     for (int dc = 0; dc < a.nd; ++dc) {
     col0 = dc * D;
     if (dc > 0) __syncthreads();  // every wave is done with the previous slice
-    // ---- Q and K rows of the slice (rows past S read 0) -------------------------
-    for (int idx = tid; idx < RP * CH; idx += kThreads) {
-        const int r = idx / CH, c = idx - (idx / CH) * CH;
-        lds_st16(sq + chunk_off_w<D>(r, c), buf_ld16(rq, (uint32_t)(r * a.qss + col0 + c * 8) * 2));
-        lds_st16(sk + chunk_off_w<D>(r, c), buf_ld16(rk, (uint32_t)(r * a.kss + col0 + c * 8) * 2));
-    }
+    commit_qk();
     __syncthreads();
+    if (dc + 1 < a.nd) issue_qk(col0 + D);
     for (int t = wave; t < 2 * ntile; t += kWaves) {
         f32x4 acc[NDT];
 #pragma unroll

@@ -40,8 +40,16 @@ constexpr int kKqBwdWaves = 8;
 // past the sample, calls store(i, c, dl) once.  PROBS: dL = P (G - sum G P),
 // the sum reduced per wave and then over the waves in a fixed order through
 // `sred` (kKqBwdWaves floats of LDS); otherwise dL = G; illegal entries 0.
-template <int RP, bool PROBS, typename Store>
-__device__ __forceinline__ void kq_bwd_dl(const KqBwdArgs& a, int b, lds_t* sred, Store store) {
+//
+// Logits with G rows that are not 16-byte aligned (S % 4 != 0, as at the
+// reference Move head's 101 squares), S <= 110 and contiguous mask rows:
+// the sample's S * S entries are read flat instead, in groups of 4 per lane
+// (one 4-byte mask word, one 16-byte or four 4-byte G loads), after every
+// piece has been zeroed, and each entry goes to LDS through store1(i, j,
+// value).  (The piece path would issue 8 scattered 4-byte G loads and 8
+// byte loads of the mask per piece; byte loads are the costly part.)
+template <int RP, bool PROBS, typename Store, typename Store1>
+__device__ __forceinline__ void kq_bwd_dl(const KqBwdArgs& a, int b, lds_t* sred, Store store, Store1 store1) {
     constexpr int kThreads = kKqBwdThreads, kWaves = kKqBwdWaves;
     constexpr uint32_t kOut = 0xfffffff0u;
     constexpr int GC = RP / 8;  // 8-entry pieces per dL row
@@ -53,6 +61,70 @@ __device__ __forceinline__ void kq_bwd_dl(const KqBwdArgs& a, int b, lds_t* sred
     const rsrc_t rp = make_rsrc(PROBS ? a.probs + b * a.psb : a.grad, PROBS ? (uint32_t)(S * S * 4) : 0u);
     const uint8_t* const mrow0 = a.mask ? a.mask + b * a.msb : nullptr;
     const rsrc_t rm = make_rsrc(mrow0 ? mrow0 : a.mask, mrow0 ? (uint32_t)((S - 1) * a.mss + S) : 0u);
+
+    constexpr int FG = 6;  // 4-entry groups per thread of the flat path: S <= 110
+    if (!PROBS && !a.grad_vec && S * S + 3 <= FG * 4 * kThreads && (!mrow0 || a.mss == S)) {
+        const int n = S * S;
+        // Group k holds entries e = 4k - sh .. 4k - sh + 3 (those in [0, n)),
+        // sh the mask's byte misalignment: the group's 4 mask bytes are one
+        // 4-byte-aligned word.  Its G entries are one 16-byte-aligned load
+        // when the G and mask bases agree (contiguous tensors do), else four
+        // 4-byte loads.  The two partial groups at the ends load bytes.
+        // (without a mask, sh aligns the G groups instead)
+        const uintptr_t gbase = (uintptr_t)(a.grad + b * a.gsb);
+        const int sh = mrow0 ? (int)((uintptr_t)mrow0 & 3) : (int)((gbase >> 2) & 3);
+        const bool g16 = ((gbase - 4 * sh) & 15) == 0;  // (uniform)
+        f32x4 gv[FG];
+        uint32_t mw[FG];
+#pragma unroll
+        for (int u = 0; u < FG; ++u) {
+            const int off = 4 * (tid + u * kThreads) - sh;  // first entry of the group
+            const bool full = off >= 0 && off + 4 <= n;
+            if (g16) {
+                gv[u] = as_f32x4(buf_ld16(rg, full ? (uint32_t)off * 4 : kOut));
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    gv[u][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, full ? (off + r) * 4 : (int)kOut, 0, 0));
+            }
+            mw[u] = !mrow0 ? 0x01010101u : __builtin_amdgcn_raw_buffer_load_b32(rm, full ? off : (int)kOut, 0, 0);
+            if (!full && off + 4 > 0 && off < n) {  // a partial group (two lanes of the workgroup)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const bool in = off + r >= 0 && off + r < n;
+                    gv[u][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, in ? (off + r) * 4 : (int)kOut, 0, 0));
+                    if (mrow0) mw[u] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rm, in ? off + r : (int)kOut, 0, 0) << (8 * r);
+                }
+            }
+        }
+        const float zero8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < PERT; ++u) {
+            const int idx = tid + u * kThreads;
+            if (idx < RP * GC) store(idx / GC, idx - (idx / GC) * GC, zero8);
+        }
+        __syncthreads();  // the zeros land before the entries
+#pragma unroll
+        for (int u = 0; u < FG; ++u) {
+            int e = 4 * (tid + u * kThreads) - sh;
+            if (e >= n) break;  // (this and every later group of the thread)
+            int i = 0, j = e;  // e < 0 (the first group): j reaches 0 at e = 0
+            if (e >= 0) {
+                i = e / S;
+                j = e - i * S;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (e >= 0 && e < n) store1(i, j, ((mw[u] >> (8 * r)) & 0xffu) != 0u ? gv[u][r] : 0.f);
+                ++e;
+                if (++j == S) {
+                    j = 0;
+                    ++i;
+                }
+            }
+        }
+        return;
+    }
 
     // ---- phase 1: dL into LDS -------------------------------------------------
     // Thread t handles dL chunks t, t + 512, ...: row i = idx / GC, columns

@@ -56,10 +56,13 @@ void kq_bwd_fp32(KqBwdArgs a) {
     const int b = blockIdx.x;
     const int S = a.S;
 
-    kq_bwd_dl<RP, PROBS>(a, b, sred, [&](int i, int c, const float (&dl)[8]) {
-        lds_st16(sg + fchunk<RP>(i, 2 * c) * 4, __builtin_bit_cast(u32x4, f32x4{dl[0], dl[1], dl[2], dl[3]}));
-        lds_st16(sg + fchunk<RP>(i, 2 * c + 1) * 4, __builtin_bit_cast(u32x4, f32x4{dl[4], dl[5], dl[6], dl[7]}));
-    });
+    kq_bwd_dl<RP, PROBS>(
+        a, b, sred,
+        [&](int i, int c, const float (&dl)[8]) {
+            lds_st16(sg + fchunk<RP>(i, 2 * c) * 4, __builtin_bit_cast(u32x4, f32x4{dl[0], dl[1], dl[2], dl[3]}));
+            lds_st16(sg + fchunk<RP>(i, 2 * c + 1) * 4, __builtin_bit_cast(u32x4, f32x4{dl[4], dl[5], dl[6], dl[7]}));
+        },
+        [&](int i, int j, float v) { lds_st4(sg + felem<RP>(i, j) * 4, __builtin_bit_cast(uint32_t, v)); });
 
     const rsrc_t rq = make_rsrc(static_cast<const float*>(a.q) + b * a.qsb, (uint32_t)(((S - 1) * a.qss + a.Dfull) * 4));
     const rsrc_t rk = make_rsrc(static_cast<const float*>(a.k) + b * a.ksb, (uint32_t)(((S - 1) * a.kss + a.Dfull) * 4));
@@ -70,16 +73,37 @@ void kq_bwd_fp32(KqBwdArgs a) {
         return __builtin_bit_cast(float, lds_ld4(base + felem<DC>(r, c) * 4));
     };
     const int ntile = (S + 15) >> 4;
+    // q / k rows of a slice, in registers between the loads and the LDS
+    // stores (rows past S read 0): each next slice's loads go out before the
+    // current slice's products, so they wait under them
+    constexpr int QKU = (RP * CH4 + kThreads - 1) / kThreads;  // chunks per thread and tensor
+    u32x4 qn[QKU], kn[QKU];
+    auto issue_qk = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < QKU; ++u) {
+            const int idx = tid + u * kThreads;
+            const int r = idx / CH4, c = idx - (idx / CH4) * CH4;
+            const bool in = idx < RP * CH4;
+            qn[u] = buf_ld16(rq, in ? (uint32_t)(r * a.qss + c0 + c * 4) * 4 : 0xfffffff0u);
+            kn[u] = buf_ld16(rk, in ? (uint32_t)(r * a.kss + c0 + c * 4) * 4 : 0xfffffff0u);
+        }
+    };
+    issue_qk(0);
 
     for (int dc = 0; dc < a.nd; ++dc) {
         const int col0 = dc * DC;
         if (dc > 0) __syncthreads();  // every wave is done with the previous slice
-        for (int idx = tid; idx < RP * CH4; idx += kThreads) {
+#pragma unroll
+        for (int u = 0; u < QKU; ++u) {
+            const int idx = tid + u * kThreads;
             const int r = idx / CH4, c = idx - (idx / CH4) * CH4;
-            lds_st16(sq + fchunk<DC>(r, c) * 4, buf_ld16(rq, (uint32_t)(r * a.qss + col0 + c * 4) * 4));
-            lds_st16(sk + fchunk<DC>(r, c) * 4, buf_ld16(rk, (uint32_t)(r * a.kss + col0 + c * 4) * 4));
+            if (idx < RP * CH4) {
+                lds_st16(sq + fchunk<DC>(r, c) * 4, qn[u]);
+                lds_st16(sk + fchunk<DC>(r, c) * 4, kn[u]);
+            }
         }
         __syncthreads();
+        if (dc + 1 < a.nd) issue_qk(col0 + DC);
         // wave passes over the output tiles: dq^T tiles 0 .. ntile-1, then dk^T
         for (int t = wave; t < 2 * ntile; t += kWaves) {
             // LDS bases through opaque copies: otherwise every per-lane
@@ -97,6 +121,7 @@ void kq_bwd_fp32(KqBwdArgs a) {
                 const int row = t * 16 + m;
 #pragma unroll
                 for (int c = 0; c < NC; ++c) {
+                    if (c * 16 >= S) break;  // zero rows of dL and k (uniform)
                     __builtin_amdgcn_sched_barrier(0);
                     const f32x4 dl4 = as_f32x4(lds_ld16(sgt + fchunk<RP>(row, 4 * c + g) * 4));
 #pragma unroll
@@ -119,6 +144,7 @@ void kq_bwd_fp32(KqBwdArgs a) {
                 const int col = jt * 16 + m;
 #pragma unroll
                 for (int c = 0; c < NC; ++c) {
+                    if (c * 16 >= S) break;  // zero rows of dL and q (uniform)
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {

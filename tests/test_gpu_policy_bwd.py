@@ -54,8 +54,10 @@ def assert_grad_close(got: torch.Tensor, ref: np.ndarray, what: str) -> None:
         assert fro <= rel_fro, f"{what}: relative Frobenius error {fro:.3e} > {rel_fro}"
 
 
-def run_case(cuda, b, s, d, dtype, output, p_legal=0.02, seed=0, scale=None, empty_sample=False, mask_view=False):
-    _announce(f"kq bwd b={b} s={s} d={d} {dtype} {output} p={p_legal} empty={empty_sample} view={mask_view}")
+def run_case(cuda, b, s, d, dtype, output, p_legal=0.02, seed=0, scale=None, empty_sample=False, mask_view=False,
+             grad_view=False):
+    _announce(f"kq bwd b={b} s={s} d={d} {dtype} {output} p={p_legal} empty={empty_sample} view={mask_view} "
+              f"grad_view={grad_view}")
     q = randn((b, s, d), seed, dtype)
     k = randn((b, s, d), seed + 1, dtype)
     mask = None if p_legal is None else legal_mask(b, s, seed + 2, p_legal)
@@ -64,6 +66,10 @@ def run_case(cuda, b, s, d, dtype, output, p_legal=0.02, seed=0, scale=None, emp
     grad = randn((b, s * s), seed + 3, torch.float32)
     sc = scale if scale is not None else d**-0.5
     qd, kd, gd = q.to(cuda), k.to(cuda), grad.to(cuda)
+    if grad_view:  # rows of a wider buffer, one NaN before each: 4-byte aligned, not 16
+        big = torch.full((b, s * s + 1), float("nan"), dtype=torch.float32)
+        big[:, 1:] = grad
+        gd = big.to(cuda)[:, 1:]
     md = None
     if mask is not None:
         if mask_view:  # rows of a wider buffer: row stride s + 3, not a multiple of 4
@@ -126,20 +132,35 @@ def test_dims(cuda, d, dtype):
     run_case(cuda, 8, 100, d, dtype, "logits", p_legal=0.1, seed=50 + d)
 
 
+@pytest.mark.parametrize("s", [100, 101])
 @pytest.mark.parametrize("output", ["logits", "probs"])
-def test_no_mask(cuda, output):
-    run_case(cuda, 8, 100, 64, torch.bfloat16, output, p_legal=None, seed=60)
+def test_no_mask(cuda, s, output):
+    run_case(cuda, 8, s, 64, torch.bfloat16, output, p_legal=None, seed=60)
 
 
+@pytest.mark.parametrize("s", [100, 101])
 @pytest.mark.parametrize("output", ["logits", "probs"])
-def test_sample_without_legal_moves_gets_zero(cuda, output):
-    run_case(cuda, 8, 100, 64, torch.bfloat16, output, seed=61, empty_sample=True)
+def test_sample_without_legal_moves_gets_zero(cuda, s, output):
+    run_case(cuda, 8, s, 64, torch.bfloat16, output, seed=61, empty_sample=True)
 
 
-@pytest.mark.parametrize("s", [17, 100])
-def test_mask_rows_of_a_wider_buffer(cuda, s):
-    """Mask rows not 4-byte aligned: the byte-wise legality path."""
-    run_case(cuda, 8, s, 64, torch.bfloat16, "probs", p_legal=0.3, seed=62, mask_view=True)
+@pytest.mark.parametrize("s", [17, 100, 101])
+@pytest.mark.parametrize("output", ["logits", "probs"])
+def test_mask_rows_of_a_wider_buffer(cuda, s, output):
+    """Mask rows not 4-byte aligned: the byte-wise legality path (and, for
+    the logits at S % 4 != 0, the flat one)."""
+    run_case(cuda, 8, s, 64, torch.bfloat16, output, p_legal=0.3, seed=62, mask_view=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("s", [100, 101])
+@pytest.mark.parametrize("output", ["logits", "probs"])
+def test_gradient_rows_not_16_byte_aligned(cuda, dtype, s, output):
+    """G rows 4-byte but not 16-byte aligned (a view one float into a wider
+    buffer, NaN around it): the logits gradient reads the sample's entries
+    flat, one per lane, the probabilities gradient piece by piece with 4-byte
+    loads; nothing outside the view is read."""
+    run_case(cuda, 8, s, 64, dtype, output, p_legal=0.2, seed=63 + s, grad_view=True)
 
 
 def test_autograd_takes_the_hip_backward(cuda):
