@@ -73,6 +73,7 @@ void kq_bwd_fp32(KqBwdArgs a) {
         return __builtin_bit_cast(float, lds_ld4(base + felem<DC>(r, c) * 4));
     };
     const int ntile = (S + 15) >> 4;
+    const int ncs = min(NC, ntile);  // 16-square chunks holding squares < S
     // q / k rows of a slice, in registers between the loads and the LDS
     // stores (rows past S read 0): each next slice's loads go out before the
     // current slice's products, so they wait under them
@@ -119,16 +120,34 @@ void kq_bwd_fp32(KqBwdArgs a) {
                 // dq^T[d][i] = sum_j k[j][d] dL[i][j]; column i = 16t + m,
                 // k-step (c, e) covers j = 16c + 4g' + e
                 const int row = t * 16 + m;
-#pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    if (c * 16 >= S) break;  // zero rows of dL and k (uniform)
-                    __builtin_amdgcn_sched_barrier(0);
-                    const f32x4 dl4 = as_f32x4(lds_ld16(sgt + fchunk<RP>(row, 4 * c + g) * 4));
+                // operands of chunk c + 1 read before the MFMAs of chunk c
+                f32x4 dlc;
+                float kc[NDT][4];
+                auto ld_dq = [&](int c, f32x4& dl, float (&kk)[NDT][4]) {
+                    dl = as_f32x4(lds_ld16(sgt + fchunk<RP>(row, 4 * c + g) * 4));
 #pragma unroll
                     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            acc[dt] = mma_f32(ld_elem(skt, 16 * c + 4 * g + e, dcol(dt)), dl4[e], acc[dt]);
+                        for (int e = 0; e < 4; ++e) kk[dt][e] = ld_elem(skt, 16 * c + 4 * g + e, dcol(dt));
+                };
+                ld_dq(0, dlc, kc);
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    if (c >= ncs) break;  // zero rows of dL and k (uniform)
+                    f32x4 dln;
+                    float kn[NDT][4];
+                    if (c + 1 < ncs) ld_dq(c + 1, dln, kn);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[dt] = mma_f32(kc[dt][e], dlc[e], acc[dt]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    dlc = dln;
+#pragma unroll
+                    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) kc[dt][e] = kn[dt][e];
                 }
                 const uint32_t base = (uint32_t)(row * a.dqss + col0 + g * QD) * 4;
 #pragma unroll
@@ -142,16 +161,33 @@ void kq_bwd_fp32(KqBwdArgs a) {
                 // k-step (c, e) covers i = 16c + 4g' + e
                 const int jt = t - ntile;
                 const int col = jt * 16 + m;
+                // operands of chunk c + 1 read before the MFMAs of chunk c
+                float dlc[4], qc[NDT][4];
+                auto ld_dk = [&](int c, float (&dl)[4], float (&qq)[NDT][4]) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        dl[e] = __builtin_bit_cast(float, lds_ld4(sgt + felem<RP>(16 * c + 4 * g + e, col) * 4));
+#pragma unroll
+                        for (int dt = 0; dt < NDT; ++dt) qq[dt][e] = ld_elem(sqt, 16 * c + 4 * g + e, dcol(dt));
+                    }
+                };
+                ld_dk(0, dlc, qc);
 #pragma unroll
                 for (int c = 0; c < NC; ++c) {
-                    if (c * 16 >= S) break;  // zero rows of dL and q (uniform)
+                    if (c >= ncs) break;  // zero rows of dL and q (uniform)
+                    float dln[4], qn[NDT][4];
+                    if (c + 1 < ncs) ld_dk(c + 1, dln, qn);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+#pragma unroll
+                        for (int dt = 0; dt < NDT; ++dt) acc[dt] = mma_f32(qc[dt][e], dlc[e], acc[dt]);
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const float dle = __builtin_bit_cast(float, lds_ld4(sgt + felem<RP>(16 * c + 4 * g + e, col) * 4));
+                        dlc[e] = dln[e];
 #pragma unroll
-                        for (int dt = 0; dt < NDT; ++dt)
-                            acc[dt] = mma_f32(ld_elem(sqt, 16 * c + 4 * g + e, dcol(dt)), dle, acc[dt]);
+                        for (int dt = 0; dt < NDT; ++dt) qc[dt][e] = qn[dt][e];
                     }
                 }
                 const uint32_t base = (uint32_t)(col * a.dkss + col0 + g * QD) * 4;
