@@ -481,6 +481,12 @@ def time_kq_backward(torch, ops, batch, dev, steps, warmup):
     ms = _mean_launch_ms(torch, lambda: ops.kq_policy_backward(q2, k2, g2, m2), max(5, steps // 5), 3)
     legs["logits_move_ref_d384"] = _leg("policy head backward at the reference Move head's shape (101 squares, d=384), bf16",
                                         ms, batch * (s2 * s2 * 4 + s2 * s2 + 4 * s2 * d2 * 2), batch)
+    # the same head in fp32, the precision the reference's Move trainer runs it in
+    q2f, k2f = q2.float(), k2.float()
+    ms = _mean_launch_ms(torch, lambda: ops.kq_policy_backward(q2f, k2f, g2, m2), max(5, steps // 5), 3)
+    legs["logits_move_ref_d384_fp32"] = _leg(
+        "policy head backward at the reference Move head's shape (101 squares, d=384), fp32 q/k", ms,
+        batch * (s2 * s2 * 4 + s2 * s2 + 4 * s2 * d2 * 4), batch)
     return {"config": "C2 policy head backward, B=4096, 100x100, d=64, bf16 q/k, fp32 gradient", "legs": legs}
 
 
