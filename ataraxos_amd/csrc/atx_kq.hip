@@ -92,6 +92,7 @@ void kq_policy(KqArgs a) {
     constexpr int QKC = ROWS * kSliceChunks;               // chunks per tensor and slice
     constexpr int QIT = (QKC + kThreads - 1) / kThreads;   // per thread
     constexpr int MIT = (ROWS * ROWS / 16 + kThreads - 1) / kThreads;  // legality chunks per thread
+    constexpr int MG = (ROWS * ROWS / 4 + 1 + kThreads - 1) / kThreads;  // legality words per thread (grouped)
     constexpr int NLB = (R * NT * 4 + 31) / 32;
 
     lds_t* const sk = lds_base();
@@ -119,6 +120,15 @@ void kq_policy(KqArgs a) {
     // ---- slice sc of Q and K (and, with the first, the legality bytes) ->
     //      LDS.  Chunk c of row r sits at c ^ ((r >> 1) & 7): the 16 rows one
     //      MFMA operand read touches fall in distinct bank groups. ----------
+    // Legality with contiguous rows that are not 16-byte aligned (S % 4 != 0,
+    // as at the reference's 101 squares): the sample's S*S bytes in groups of
+    // 4, group k = bytes 4k - sh .. 4k - sh + 3 with sh the base's
+    // misalignment, so that each group is one aligned 4-byte load (the two
+    // partial groups at the ends load bytes); the bytes are then placed in
+    // the [S][SP] LDS rows.  (One byte load per square was the cost.)
+    const uint8_t* const mbase = a.mask ? a.mask + b * a.msb : nullptr;
+    const bool grouped = mbase && !a.mask_lin && a.mss == S;  // (uniform)
+    const int msh = (int)((uintptr_t)mbase & 3);
     auto stage = [&](int sc) {
         u32x4 qv[QIT], kv[QIT], mv[MIT];
 #pragma unroll
@@ -152,7 +162,7 @@ void kq_policy(KqArgs a) {
                 const int idx = tid + it * kThreads;
                 if (idx * 16 < S * S) lds_st16(smask + idx * 16, mv[it]);
             }
-        } else if (sc == 0) {  // any layout, or no mask (= every square legal)
+        } else if (sc == 0 && !grouped) {  // any layout, or no mask (= every square legal)
             const uint8_t* mb = a.mask ? a.mask + b * a.msb : nullptr;
             for (int idx = tid; idx < S * SP; idx += kThreads) {
                 const int i = idx / SP, j = idx - i * SP;
@@ -191,6 +201,49 @@ void kq_policy(KqArgs a) {
             __builtin_amdgcn_sched_barrier(0);
         }
     };
+    if (grouped) {  // (before the slices: nothing else is live yet)
+        const int n = S * S;
+        const rsrc_t rm = make_rsrc(mbase, (uint32_t)n);
+        uint32_t mw[MG];
+#pragma unroll
+        for (int it = 0; it < MG; ++it) {
+            const int off = 4 * (tid + it * kThreads) - msh;
+            const bool full = off >= 0 && off + 4 <= n;
+            mw[it] = __builtin_amdgcn_raw_buffer_load_b32(rm, full ? off : (int)0xfffffff0u, 0, 0);
+            if (!full && off + 4 > 0 && off < n) {  // a partial group (two threads of the workgroup)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const bool in = off + r >= 0 && off + r < n;
+                    mw[it] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rm, in ? off + r : (int)0xfffffff0u, 0, 0) << (8 * r);
+                }
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < MG; ++it) {
+            int e = 4 * (tid + it * kThreads) - msh;
+            if (e >= n) break;  // (this and every later group of the thread)
+            int i = 0, j = e;   // e < 0 (the first group): j reaches 0 at e = 0
+            if (e >= 0) {
+                i = e / S;
+                j = e - i * S;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (e >= 0 && e < n) lds_st1(smask + i * SP + j, ((mw[it] >> (8 * r)) & 0xffu) != 0u ? 1u : 0u);
+                ++e;
+                if (++j == S) {
+                    j = 0;
+                    ++i;
+                }
+            }
+        }
+        // the rows' padding columns S .. SP - 1: illegal
+        for (int idx = tid; idx < S * (SP - S); idx += kThreads) {
+            const int i = idx / (SP - S);
+            lds_st1(smask + i * SP + S + (idx - i * (SP - S)), 0u);
+        }
+        // (visible to every wave after the first slice's barrier)
+    }
     if constexpr (!MULTI) {
         stage(0);
         products(true);
@@ -304,9 +357,36 @@ void kq_policy(KqArgs a) {
     if (a.out_vec && SP == S) {  // plain (L2-cached) stores: measured faster here than streaming ones
         for (int idx = tid; idx * 4 < S * S; idx += kThreads) buf_st16_cached(ro, idx * 16, lds_ld16(sout + idx * 16));
     } else {
-        for (int idx = tid; idx < S * S; idx += kThreads) {
-            const int i = idx / S, j = idx - i * S;
-            buf_st4_cached(ro, idx * 4, lds_ld4(sout + (i * SP + j) * 4));
+        // Groups of 4 entries, group k = entries 4k - sh .. 4k - sh + 3 with
+        // sh the output's misalignment in floats: one aligned 16-byte store
+        // each (the two partial groups at the ends store single floats).
+        const int n = S * S;
+        const int osh = (int)(((uintptr_t)(a.out + b * a.osb) >> 2) & 3);
+        const int ng = (n + osh + 3) >> 2;
+        for (int k = tid; k < ng; k += kThreads) {
+            const int off = 4 * k - osh;
+            int e = off, i = 0, j = off;  // off < 0 (the first group): j reaches 0 at e = 0
+            if (e >= 0) {
+                i = e / S;
+                j = e - i * S;
+            }
+            uint32_t v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                v[r] = (e >= 0 && e < n) ? lds_ld4(sout + (i * SP + j) * 4) : 0u;
+                ++e;
+                if (++j == S) {
+                    j = 0;
+                    ++i;
+                }
+            }
+            if (off >= 0 && off + 4 <= n) {
+                buf_st16_cached(ro, (uint32_t)off * 4, u32x4{v[0], v[1], v[2], v[3]});
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (off + r >= 0 && off + r < n) buf_st4_cached(ro, (uint32_t)(off + r) * 4, v[r]);
+            }
         }
     }
 }

@@ -124,3 +124,45 @@ def test_equal_logits_split_evenly(cuda):
     for i in range(b):
         legal = mask[i].reshape(-1)
         np.testing.assert_allclose(out[i][legal].numpy(), 1.0 / n[i].item(), rtol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("d", [64, 384])
+@pytest.mark.parametrize("output", ["probs", "logits"])
+def test_reference_move_head_shape(cuda, dtype, d, output):
+    """101 squares (the reference Move network): the sample's mask bytes and
+    output row start at every alignment mod 16 across 9 samples, which the
+    kernel reads and writes in 4-entry groups phased to each base."""
+    out, ref, mask = _run(cuda, 9, 101, d, dtype, p=0.1, seed=500 + d, output=output)
+    if output == "probs":
+        _check_probs(out, ref, mask, dtype)
+    else:
+        o = out.double().numpy()
+        illegal = ~mask.reshape(9, -1).numpy()
+        assert (o[illegal] == np.float32(-1e10)).all()
+        err = np.abs(o[~illegal] - ref[~illegal]).max()
+        assert err <= (1e-5 * np.abs(ref[~illegal]).max() if dtype == torch.float32 else LOWP_ABS_TOL)
+
+
+@pytest.mark.parametrize("s", [100, 101])
+@pytest.mark.parametrize("output", ["probs", "logits"])
+def test_misaligned_mask_and_output_views(cuda, s, output):
+    """A mask that starts 3 bytes into its buffer and an output that starts
+    one float into its own (contiguous views, NaN around the output): the
+    results match the aligned call bit for bit and nothing outside the
+    output view is written."""
+    b, d = 6, 64
+    _announce(f"kq misaligned views s={s} {output}")
+    q = randn((b, s, d), 70 + s, torch.bfloat16).to(cuda)
+    k = randn((b, s, d), 71 + s, torch.bfloat16).to(cuda)
+    mask = legal_mask(b, s, 72 + s, 0.1)
+    mbig = torch.zeros(b * s * s + 3, dtype=torch.bool)
+    mbig[3:] = mask.reshape(-1)
+    mview = mbig.to(cuda)[3:].view(b, s, s)
+    obig = torch.full((b * s * s + 2,), float("nan"), dtype=torch.float32, device=cuda)
+    oview = obig[1:1 + b * s * s].view(b, s * s)
+    ops.kq_policy(q, k, mview, output=output, out=oview)
+    want = ops.kq_policy(q, k, mask.to(cuda), output=output)
+    torch.cuda.synchronize()
+    assert torch.isnan(obig[0]) and torch.isnan(obig[-1]), "written outside the output view"
+    assert torch.equal(oview, want)
