@@ -287,12 +287,23 @@ def time_kq(torch, ops, batch, dev, steps, warmup):
     out = torch.empty(batch, s * s, dtype=torch.float32, device=dev)
     ms = _mean_launch_ms(torch, lambda: ops.kq_policy(q, k, mask, out=out), steps, warmup)
     bytes_per_sample = 2 * s * d * 2 + s * s + s * s * 4
+    # the reference Move network's own head: 101 squares, d=384 (rows start at any alignment)
+    s2, d2 = 101, 384
+    q2 = torch.randn(batch, s2, d2, generator=g, device=dev).to(torch.bfloat16)
+    k2 = torch.randn(batch, s2, d2, generator=g, device=dev).to(torch.bfloat16)
+    m2 = torch.rand(batch, s2, s2, generator=g, device=dev) < 0.02
+    m2[:, 0, 0] |= ~m2.flatten(1).any(dim=1)
+    out2 = torch.empty(batch, s2 * s2, dtype=torch.float32, device=dev)
+    ms2 = _mean_launch_ms(torch, lambda: ops.kq_policy(q2, k2, m2, out=out2), steps, warmup)
+    bytes2 = 2 * s2 * d2 * 2 + s2 * s2 + s2 * s2 * 4
     return {
         "config": "C2 KQ logits + legal mask + softmax, B=4096, 100x100, d=64, bf16 in, fp32 out",
         "samples_per_s": batch / (ms * 1e-3),
         "kernel_ms": ms,
         "achieved_gbs": batch * bytes_per_sample / (ms * 1e-3) / 1e9,
         "hbm_frac": batch * bytes_per_sample / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "move_ref_d384": _leg("policy head forward (probabilities) at the reference Move head's shape "
+                              "(B=4096, 101 squares, d=384), bf16", ms2, batch * bytes2, batch),
     }
 
 
