@@ -310,20 +310,23 @@ extern "C" int atx_kq_bwd(const AtxKqBwdParams* p, void* stream) {
     a.dqss = (int)dqss; a.dkss = (int)dkss;
     a.S = S;
     a.Dfull = D;
+    const int nkc = S <= 64 ? 2 : (S + 31) / 32;
+    // fp32 at 97 to 112 squares: 112 staged, 16-column slices (two
+    // workgroups per CU); other fp32 shapes 32 * nkc staged
+    const int rp32 = (S > 96 && S <= 112) ? 112 : 32 * nkc;
     // 16-bit: rows up to 128 wide in one slice, wider ones in 64-column
     // slices; fp32: slices of 32 or 16 columns
-    const int dslice = f32 ? (D % 32 == 0 ? 32 : 16) : (D <= 128 ? D : 64);
+    const int dslice = f32 ? (D % 32 == 0 && rp32 != 112 ? 32 : 16) : (D <= 128 ? D : 64);
     a.nd = D / dslice;
     a.scale = p->scale;
     a.mask_al4 = p->mask && ((uintptr_t)p->mask & 3) == 0 && (p->mask_stride_b & 3) == 0 && (p->mask_stride_s & 3) == 0;
     a.grad_vec = S % 4 == 0 && aligned16(p->grad) && (p->grad_stride_b & 3) == 0 &&
                  (!probs || (aligned16(p->probs) && (p->probs_stride_b & 3) == 0));
-    const int nkc = S <= 64 ? 2 : (S + 31) / 32;
-    const size_t lds = f32 ? kq_bwd_fp32_lds_bytes(dslice, nkc) : kq_bwd_lds_bytes(dslice, nkc);
+    const size_t lds = f32 ? kq_bwd_fp32_lds_bytes(dslice, rp32) : kq_bwd_lds_bytes(dslice, nkc);
     if (lds > 160 * 1024)
         ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_bwd: seq %d, dim %d need %zu bytes of LDS (> 160 KiB)", S, D, lds);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (f32) return dispatch_kq_bwd_fp32(probs, dslice, nkc, p->batch, lds, st, a);
+    if (f32) return dispatch_kq_bwd_fp32(probs, dslice, rp32, p->batch, lds, st, a);
     if (p->dtype == ATX_DTYPE_BF16)
         return probs ? dispatch_kq_bwd<__bf16, true>(dslice, nkc, p->batch, lds, st, a)
                      : dispatch_kq_bwd<__bf16, false>(dslice, nkc, p->batch, lds, st, a);

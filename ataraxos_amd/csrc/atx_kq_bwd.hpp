@@ -219,7 +219,8 @@ __device__ __forceinline__ void kq_bwd_dl(const KqBwdArgs& a, int b, lds_t* sred
 }
 
 // LDS of the fp32 kernel and its launcher (atx_kq_bwd_fp32.hip).
-size_t kq_bwd_fp32_lds_bytes(int dslice, int nkc);
-int dispatch_kq_bwd_fp32(bool probs, int dslice, int nkc, int grid, size_t lds, hipStream_t st, const KqBwdArgs& a);
+// rp: squares staged (64, 96 or 128; 112 with 16-column slices).
+size_t kq_bwd_fp32_lds_bytes(int dslice, int rp);
+int dispatch_kq_bwd_fp32(bool probs, int dslice, int rp, int grid, size_t lds, hipStream_t st, const KqBwdArgs& a);
 
 }  // namespace atx

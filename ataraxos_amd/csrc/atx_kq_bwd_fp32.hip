@@ -35,11 +35,18 @@ __device__ inline int felem(int r, int c) {  // float offset of row r, column c
     return r * W + (((c >> 2) ^ hsw_w<W>(r)) << 2) + (c & 3);
 }
 
-// NKC = 32-square chunks (S <= 32 * NKC); DC = slice width (floats).
-template <int DC, int NKC, bool PROBS>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8)))
+// RP = squares staged (S <= RP, a multiple of 16); DC = slice width
+// (floats).  RP = 112 with 16-column slices (97 to 112 squares, the
+// reference's 100 and 101): 63 KB of LDS and at most 128 VGPRs, so two
+// workgroups share a CU and one sample's loads and stores run under the
+// other's products; the other shapes take 64 to 128 KB, one per CU.
+template <int RP>
+constexpr int kq_bwd_fp32_occ() {
+    return RP == 112 ? 4 : 2;
+}
+template <int DC, int RP, bool PROBS>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kq_bwd_fp32_occ<RP>(), 8)))
 void kq_bwd_fp32(KqBwdArgs a) {
-    constexpr int RP = 32 * NKC;
     constexpr int CH4 = DC / 4;   // 4-float chunks per q / k slice row
     constexpr int NDT = DC / 16;  // output tiles of the slice
     constexpr int QD = DC / 4;    // contiguous outputs per lane
@@ -215,33 +222,36 @@ int launch(K kernel, int grid, size_t lds, hipStream_t st, const KqBwdArgs& a) {
 }
 
 template <int DC, bool PROBS>
-int by_nkc(int nkc, int grid, size_t lds, hipStream_t st, const KqBwdArgs& a) {
-    switch (nkc) {
-        case 2: return launch(kq_bwd_fp32<DC, 2, PROBS>, grid, lds, st, a);
-        case 3: return launch(kq_bwd_fp32<DC, 3, PROBS>, grid, lds, st, a);
-        case 4: return launch(kq_bwd_fp32<DC, 4, PROBS>, grid, lds, st, a);
-        default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_bwd: %d 32-square chunks", nkc);
+int by_rp(int rp, int grid, size_t lds, hipStream_t st, const KqBwdArgs& a) {
+    switch (rp) {
+        case 64: return launch(kq_bwd_fp32<DC, 64, PROBS>, grid, lds, st, a);
+        case 96: return launch(kq_bwd_fp32<DC, 96, PROBS>, grid, lds, st, a);
+        case 128: return launch(kq_bwd_fp32<DC, 128, PROBS>, grid, lds, st, a);
+        default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_bwd: fp32 with %d squares staged, %d-column slices", rp, DC);
     }
 }
 
 template <bool PROBS>
-int by_dc(int dc, int nkc, int grid, size_t lds, hipStream_t st, const KqBwdArgs& a) {
+int by_dc(int dc, int rp, int grid, size_t lds, hipStream_t st, const KqBwdArgs& a) {
+    if (rp == 112) {
+        if (dc != 16) ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_bwd: fp32 112 squares need 16-column slices (got %d)", dc);
+        return launch(kq_bwd_fp32<16, 112, PROBS>, grid, lds, st, a);
+    }
     switch (dc) {
-        case 16: return by_nkc<16, PROBS>(nkc, grid, lds, st, a);
-        case 32: return by_nkc<32, PROBS>(nkc, grid, lds, st, a);
+        case 16: return by_rp<16, PROBS>(rp, grid, lds, st, a);
+        case 32: return by_rp<32, PROBS>(rp, grid, lds, st, a);
         default: ATX_FAIL(ATX_ERR_UNSUPPORTED, "atx_kq_bwd: fp32 slice width %d", dc);
     }
 }
 
 }  // namespace
 
-size_t kq_bwd_fp32_lds_bytes(int dslice, int nkc) {
-    const size_t rp = 32 * (size_t)nkc;
-    return rp * rp * 4 + 2 * rp * dslice * 4 + kWaves * 4;
+size_t kq_bwd_fp32_lds_bytes(int dslice, int rp) {
+    return (size_t)rp * rp * 4 + 2 * (size_t)rp * dslice * 4 + kWaves * 4;
 }
 
-int dispatch_kq_bwd_fp32(bool probs, int dslice, int nkc, int grid, size_t lds, hipStream_t st, const KqBwdArgs& a) {
-    return probs ? by_dc<true>(dslice, nkc, grid, lds, st, a) : by_dc<false>(dslice, nkc, grid, lds, st, a);
+int dispatch_kq_bwd_fp32(bool probs, int dslice, int rp, int grid, size_t lds, hipStream_t st, const KqBwdArgs& a) {
+    return probs ? by_dc<true>(dslice, rp, grid, lds, st, a) : by_dc<false>(dslice, rp, grid, lds, st, a);
 }
 
 }  // namespace atx
