@@ -201,35 +201,36 @@ void kq_policy(KqArgs a) {
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    if (grouped) {  // (before the slices: nothing else is live yet)
-        const int n = S * S;
-        const rsrc_t rm = make_rsrc(mbase, (uint32_t)n);
-        uint32_t mw[MG];
+    const int n2 = S * S;
+    auto mask_issue = [&](uint32_t (&mw)[MG]) {
+        const rsrc_t rm = make_rsrc(mbase, (uint32_t)n2);
 #pragma unroll
         for (int it = 0; it < MG; ++it) {
             const int off = 4 * (tid + it * kThreads) - msh;
-            const bool full = off >= 0 && off + 4 <= n;
+            const bool full = off >= 0 && off + 4 <= n2;
             mw[it] = __builtin_amdgcn_raw_buffer_load_b32(rm, full ? off : (int)0xfffffff0u, 0, 0);
-            if (!full && off + 4 > 0 && off < n) {  // a partial group (two threads of the workgroup)
+            if (!full && off + 4 > 0 && off < n2) {  // a partial group (two threads of the workgroup)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const bool in = off + r >= 0 && off + r < n;
+                    const bool in = off + r >= 0 && off + r < n2;
                     mw[it] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rm, in ? off + r : (int)0xfffffff0u, 0, 0) << (8 * r);
                 }
             }
         }
+    };
+    auto mask_place = [&](const uint32_t (&mw)[MG]) {
 #pragma unroll
         for (int it = 0; it < MG; ++it) {
             int e = 4 * (tid + it * kThreads) - msh;
-            if (e >= n) break;  // (this and every later group of the thread)
-            int i = 0, j = e;   // e < 0 (the first group): j reaches 0 at e = 0
+            if (e >= n2) break;  // (this and every later group of the thread)
+            int i = 0, j = e;    // e < 0 (the first group): j reaches 0 at e = 0
             if (e >= 0) {
                 i = e / S;
                 j = e - i * S;
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                if (e >= 0 && e < n) lds_st1(smask + i * SP + j, ((mw[it] >> (8 * r)) & 0xffu) != 0u ? 1u : 0u);
+                if (e >= 0 && e < n2) lds_st1(smask + i * SP + j, ((mw[it] >> (8 * r)) & 0xffu) != 0u ? 1u : 0u);
                 ++e;
                 if (++j == S) {
                     j = 0;
@@ -242,15 +243,40 @@ void kq_policy(KqArgs a) {
             const int i = idx / (SP - S);
             lds_st1(smask + i * SP + S + (idx - i * (SP - S)), 0u);
         }
-        // (visible to every wave after the first slice's barrier)
-    }
+    };
     if constexpr (!MULTI) {
+        if (grouped) {  // (before the slice: nothing else is live yet; its barrier publishes the bytes)
+            uint32_t mw[MG];
+            mask_issue(mw);
+            mask_place(mw);
+        }
         stage(0);
         products(true);
-    } else {
+    } else if constexpr (sizeof(T) == 4) {  // fp32: the same order (measured 6 % faster here than the one below)
+        if (grouped) {
+            uint32_t mw[MG];
+            mask_issue(mw);
+            mask_place(mw);
+        }
         for (int sc = 0; sc < nslices; ++sc) {
             stage(sc);
             products(sc == 0);
+        }
+    } else {
+        // 16-bit: the mask words are requested before the first slice and
+        // placed after it, so both loads wait together (2-3 % faster at the
+        // reference head); the next slice's barriers (there are at least two
+        // slices) publish the bytes before the legality is read.
+        {
+            uint32_t mw[MG];
+            if (grouped) mask_issue(mw);
+            stage(0);
+            if (grouped) mask_place(mw);
+        }
+        products(true);
+        for (int sc = 1; sc < nslices; ++sc) {
+            stage(sc);
+            products(false);
         }
     }
 
