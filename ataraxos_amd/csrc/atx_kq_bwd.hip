@@ -128,7 +128,8 @@ void kq_bwd_16bit(KqBwdArgs a) {
             lds_st16(sg_ + chunk_off_w<RP>(i, c), u32x4{M::pack2(dl[0], dl[1]), M::pack2(dl[2], dl[3]),
                                                            M::pack2(dl[4], dl[5]), M::pack2(dl[6], dl[7])});
         },
-        [&](int i, int j, float v) { lds_st2(sg_ + quad_off_w<RP>(i, j), M::pack2(v, 0.f)); });
+        [&](int i, int j, float v) { lds_st2(sg_ + quad_off_w<RP>(i, j), M::pack2(v, 0.f)); },
+        sg_, RP * RSG + 2 * RP * RS);  // dL and the q / k slices: free until phase 1 ends
 
     // ---- phase 2: dq^T = K^T dL^T, dk^T = Q^T dL --------------------------------
     // Transposing reads of Q / K: input lane a4 + 4t of a 16-lane group points

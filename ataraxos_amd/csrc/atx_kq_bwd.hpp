@@ -48,8 +48,15 @@ constexpr int kKqBwdWaves = 8;
 // piece has been zeroed, and each entry goes to LDS through store1(i, j,
 // value).  (The piece path would issue 8 scattered 4-byte G loads and 8
 // byte loads of the mask per piece; byte loads are the costly part.)
+//
+// The probabilities gradient takes the flat path too when `scratch` (LDS
+// that is free during this phase, `scratch_bytes` of it) holds the sample's
+// S * S products G P as floats: they are written there flat and summed per
+// 8-entry piece in the piece path's (row, column) order, so the sum depends
+// on the sample's data only, not on where its rows start.
 template <int RP, bool PROBS, typename Store, typename Store1>
-__device__ __forceinline__ void kq_bwd_dl(const KqBwdArgs& a, int b, lds_t* sred, Store store, Store1 store1) {
+__device__ __forceinline__ void kq_bwd_dl(const KqBwdArgs& a, int b, lds_t* sred, Store store, Store1 store1,
+                                          lds_t* scratch, int scratch_bytes) {
     constexpr int kThreads = kKqBwdThreads, kWaves = kKqBwdWaves;
     constexpr uint32_t kOut = 0xfffffff0u;
     constexpr int GC = RP / 8;  // 8-entry pieces per dL row
@@ -63,7 +70,8 @@ __device__ __forceinline__ void kq_bwd_dl(const KqBwdArgs& a, int b, lds_t* sred
     const rsrc_t rm = make_rsrc(mrow0 ? mrow0 : a.mask, mrow0 ? (uint32_t)((S - 1) * a.mss + S) : 0u);
 
     constexpr int FG = 6;  // 4-entry groups per thread of the flat path: S <= 110
-    if (!PROBS && !a.grad_vec && S * S + 3 <= FG * 4 * kThreads && (!mrow0 || a.mss == S)) {
+    if (!a.grad_vec && S * S + 3 <= FG * 4 * kThreads && (!mrow0 || a.mss == S) &&
+        (!PROBS || S * S * 4 <= scratch_bytes)) {
         const int n = S * S;
         // Group k holds entries e = 4k - sh .. 4k - sh + 3 (those in [0, n)),
         // sh the mask's byte misalignment: the group's 4 mask bytes are one
@@ -74,7 +82,8 @@ __device__ __forceinline__ void kq_bwd_dl(const KqBwdArgs& a, int b, lds_t* sred
         const uintptr_t gbase = (uintptr_t)(a.grad + b * a.gsb);
         const int sh = mrow0 ? (int)((uintptr_t)mrow0 & 3) : (int)((gbase >> 2) & 3);
         const bool g16 = ((gbase - 4 * sh) & 15) == 0;  // (uniform)
-        f32x4 gv[FG];
+        const bool p16 = PROBS && (((uintptr_t)(a.probs + b * a.psb) - 4 * sh) & 15) == 0;
+        f32x4 gv[FG], pv[PROBS ? FG : 1];
         uint32_t mw[FG];
 #pragma unroll
         for (int u = 0; u < FG; ++u) {
@@ -87,15 +96,54 @@ __device__ __forceinline__ void kq_bwd_dl(const KqBwdArgs& a, int b, lds_t* sred
                 for (int r = 0; r < 4; ++r)
                     gv[u][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, full ? (off + r) * 4 : (int)kOut, 0, 0));
             }
+            if constexpr (PROBS) {
+                if (p16) {
+                    pv[u] = as_f32x4(buf_ld16(rp, full ? (uint32_t)off * 4 : kOut));
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        pv[u][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, full ? (off + r) * 4 : (int)kOut, 0, 0));
+                }
+            }
             mw[u] = !mrow0 ? 0x01010101u : __builtin_amdgcn_raw_buffer_load_b32(rm, full ? off : (int)kOut, 0, 0);
             if (!full && off + 4 > 0 && off < n) {  // a partial group (two lanes of the workgroup)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const bool in = off + r >= 0 && off + r < n;
                     gv[u][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rg, in ? (off + r) * 4 : (int)kOut, 0, 0));
+                    if constexpr (PROBS)
+                        pv[u][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, in ? (off + r) * 4 : (int)kOut, 0, 0));
                     if (mrow0) mw[u] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rm, in ? off + r : (int)kOut, 0, 0) << (8 * r);
                 }
             }
+        }
+        float sigma = 0.f;
+        if constexpr (PROBS) {
+            // G P of every entry, flat, then summed per piece in row order
+#pragma unroll
+            for (int u = 0; u < FG; ++u)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int e = 4 * (tid + u * kThreads) - sh + r;
+                    if (e >= 0 && e < n) lds_st4(scratch + e * 4, __builtin_bit_cast(uint32_t, gv[u][r] * pv[u][r]));
+                }
+            __syncthreads();
+            float part = 0.f;
+#pragma unroll
+            for (int u = 0; u < PERT; ++u) {
+                const int idx = tid + u * kThreads;
+                const int i = idx / GC, j0 = (idx - (idx / GC) * GC) * 8;
+                if (idx < RP * GC && i < S && j0 < S)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (j0 + e < S) part += __builtin_bit_cast(float, lds_ld4(scratch + (i * S + j0 + e) * 4));
+            }
+#pragma unroll
+            for (int x = 32; x >= 1; x >>= 1) part += shfl_xor(part, x);
+            if (lane == 0) lds_st4(sred + wave * 4, __builtin_bit_cast(uint32_t, part));
+            __syncthreads();  // (also: every wave is done reading the scratch)
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) sigma += __builtin_bit_cast(float, lds_ld4(sred + w * 4));
         }
         const float zero8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -115,7 +163,10 @@ __device__ __forceinline__ void kq_bwd_dl(const KqBwdArgs& a, int b, lds_t* sred
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                if (e >= 0 && e < n) store1(i, j, ((mw[u] >> (8 * r)) & 0xffu) != 0u ? gv[u][r] : 0.f);
+                if (e >= 0 && e < n) {
+                    const float x = PROBS ? pv[u][r] * (gv[u][r] - sigma) : gv[u][r];
+                    store1(i, j, ((mw[u] >> (8 * r)) & 0xffu) != 0u ? x : 0.f);
+                }
                 ++e;
                 if (++j == S) {
                     j = 0;

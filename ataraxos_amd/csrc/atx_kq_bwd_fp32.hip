@@ -69,7 +69,8 @@ void kq_bwd_fp32(KqBwdArgs a) {
             lds_st16(sg + fchunk<RP>(i, 2 * c) * 4, __builtin_bit_cast(u32x4, f32x4{dl[0], dl[1], dl[2], dl[3]}));
             lds_st16(sg + fchunk<RP>(i, 2 * c + 1) * 4, __builtin_bit_cast(u32x4, f32x4{dl[4], dl[5], dl[6], dl[7]}));
         },
-        [&](int i, int j, float v) { lds_st4(sg + felem<RP>(i, j) * 4, __builtin_bit_cast(uint32_t, v)); });
+        [&](int i, int j, float v) { lds_st4(sg + felem<RP>(i, j) * 4, __builtin_bit_cast(uint32_t, v)); },
+        sg, RP * RP * 4);  // dL: free until phase 1 ends
 
     const rsrc_t rq = make_rsrc(static_cast<const float*>(a.q) + b * a.qsb, (uint32_t)(((S - 1) * a.qss + a.Dfull) * 4));
     const rsrc_t rk = make_rsrc(static_cast<const float*>(a.k) + b * a.ksb, (uint32_t)(((S - 1) * a.kss + a.Dfull) * 4));
