@@ -298,3 +298,24 @@ def test_unsupported_dims_fall_back(cuda):
     qa = qb.clone().requires_grad_(True)
     masked_policy_logits(qa, qb, None).float().sum().backward()
     assert torch.isfinite(qa.grad.float()).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("output", ["logits", "probs"])
+def test_result_does_not_depend_on_batch_position(cuda, dtype, output):
+    """At 101 squares a sample's G, P and mask rows start at a different
+    alignment in each batch position, and the kernel phases its loads to it.
+    The same sample at five positions (every alignment mod 16) gets
+    bit-identical gradients: the probabilities' sum runs in a fixed
+    (row, column) order whatever the alignment."""
+    b, s, d = 5, 101, 64
+    _announce(f"kq bwd batch-position independence {dtype} {output}")
+    q = randn((1, s, d), 80, dtype).expand(b, s, d).contiguous().to(cuda)
+    k = randn((1, s, d), 81, dtype).expand(b, s, d).contiguous().to(cuda)
+    mask = legal_mask(1, s, 82, 0.2).expand(b, s, s).contiguous().to(cuda)
+    grad = randn((1, s * s), 83, torch.float32).expand(b, s * s).contiguous().to(cuda)
+    probs = ops.kq_policy(q, k, mask, output="probs") if output == "probs" else None
+    dq, dk = ops.kq_policy_backward(q, k, grad, mask, output=output, probs=probs)
+    torch.cuda.synchronize()
+    for i in range(1, b):
+        assert torch.equal(dq[i], dq[0]) and torch.equal(dk[i], dk[0]), f"position {i} differs"
