@@ -240,7 +240,8 @@ def test_reference_move_policy_head_gradients(cuda, monkeypatch):
 
 
 @pytest.mark.parametrize("output", ["logits", "probs"])
-@pytest.mark.parametrize("s,d", [(100, 64), (101, 384), (33, 16), (64, 48), (128, 128), (100, 400), (17, 96)])
+@pytest.mark.parametrize("s,d", [(100, 64), (101, 384), (33, 16), (64, 48), (128, 128), (100, 400), (17, 96),
+                                 (96, 32), (97, 48), (112, 64), (113, 16)])
 def test_fp32(cuda, s, d, output):
     """fp32 q, k -- the precision the reference's Move trainer runs its policy
     head in -- through the fp32 kernel (fp32 products)."""
