@@ -166,3 +166,12 @@ def test_misaligned_mask_and_output_views(cuda, s, output):
     torch.cuda.synchronize()
     assert torch.isnan(obig[0]) and torch.isnan(obig[-1]), "written outside the output view"
     assert torch.equal(oview, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("s", [5, 17, 33, 127])
+def test_wide_head_at_odd_square_counts(cuda, dtype, s):
+    """d = 384 (rows staged in several slices) at square counts whose mask
+    rows and outputs start unaligned, from one to eight tile rows."""
+    out, ref, mask = _run(cuda, 6, s, 384, dtype, p=0.2, seed=600 + s)
+    _check_probs(out, ref, mask, dtype)
